@@ -1,0 +1,219 @@
+"""Benchmark of the fused linear + bias + GELU kernel on one MI355X.
+
+Default workload (the one the headline metric is quoted on): a single fused
+addmm + bias + exact-erf GELU, fp32, M = N = K = 4096, A row-major and
+B = W^T of a contiguous nn.Linear weight W[N,K] (strided operand), on the
+IEEE fp32 MFMA path.  A "step" is one fused kernel launch over that problem
+with the inputs already resident in HBM.
+
+Prints ONE JSON line with the throughput (TFLOP/s from 2*M*N*K), the
+roofline of the kernel (HIP-event launch durations on the launch stream
+against MI355X's dense MFMA peak) and the reference's CPU path (torch addmm
++ GELU on the host cores) as a reported baseline.  Additional workloads are
+reported under "extra" unless --no-extra is given.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+PEAK_TFLOPS = {torch.float32: 157.3, torch.bfloat16: 2516.6, torch.float16: 2516.6}
+HBM_GBPS = 8000.0
+DTYPE_NAMES = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+
+
+def _inputs(m, n, k, dtype, dev, seed, *, bias=True, w_std=None, a_std=None):
+    g = torch.Generator().manual_seed(seed)
+    a_std = k ** -0.25 if a_std is None else a_std
+    w_std = k ** -0.25 if w_std is None else w_std
+    a = (torch.randn(m, k, generator=g) * a_std).to(dtype).to(dev)
+    w = (torch.randn(n, k, generator=g) * w_std).to(dtype).to(dev)
+    b = ((torch.rand(n, generator=g) * 0.2 - 0.1).to(dtype).to(dev)) if bias else None
+    return a, w.t(), b
+
+
+def _time_launches(launch, steps: int, warmup: int):
+    """Wall-clock ms per step over `steps` launches, plus per-launch HIP-event ms."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for start, end in events:
+        start.record(stream)
+        launch()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per_launch = [s.elapsed_time(e) for s, e in events]
+    return wall_ms, per_launch
+
+
+def gemm_workload(name, m, n, k, dtype, *, steps, warmup, act="gelu", bias=True, a_std=None, w_std=None,
+                  config=None):
+    from forgeml_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    a, b, bvec = _inputs(m, n, k, dtype, dev, seed=0, bias=bias, a_std=a_std, w_std=w_std)
+    out = torch.empty(m, n, dtype=dtype, device=dev)
+    cfg = config or kernels.DEFAULT_CONFIG
+    resolved = kernels.resolve_config(m, n, k, dtype, cfg)
+
+    def launch():
+        kernels.matmul(a, b, bvec, activation=act, out=out, config=cfg)
+
+    wall_ms, per_launch = _time_launches(launch, steps, warmup)
+    avg_ms = statistics.fmean(per_launch)
+    flop = 2 * m * n * k
+    esz = a.element_size()
+    algo_bytes = (m * k + k * n + m * n + (n if bias else 0)) * esz
+    return {
+        "workload": name,
+        "shape": [m, n, k],
+        "dtype": DTYPE_NAMES[dtype],
+        "activation": act,
+        "bias": bias,
+        "tile": [resolved.block_m, resolved.block_n, resolved.block_k, resolved.num_waves],
+        "ms_per_step": wall_ms,
+        "kernel_ms_avg": avg_ms,
+        "kernel_ms_min": min(per_launch),
+        "tflops": flop / (wall_ms * 1e-3) / 1e12,
+        "kernel_tflops": flop / (avg_ms * 1e-3) / 1e12,
+        "pct_peak": 100.0 * flop / (avg_ms * 1e-3) / 1e12 / PEAK_TFLOPS[dtype],
+        "algorithmic_bytes": algo_bytes,
+        "flop": flop,
+    }
+
+
+def compiled_workload(name, model, x, *, steps, warmup):
+    """CompiledModel forward latency on the GPU (hip backend), host wall clock."""
+    import forgeml_amd
+    from forgeml_amd.measurement import measure_variants
+
+    dev = torch.device("cuda", 0)
+    model = model.to(dev).eval()
+    x = x.to(dev)
+    compiled = forgeml_amd.compile(model, (x,), backend="hip")
+    timings = measure_variants({"hip": lambda: compiled(x)}, device=dev, warmup=warmup, repeats=max(steps, 2))
+    return {
+        "workload": name,
+        "kernel_plan": sorted(set(compiled.kernel_plan.values())),
+        "median_us": timings["hip"]["median_ms"] * 1e3,
+        "p95_us": timings["hip"]["p95_ms"] * 1e3,
+    }
+
+
+def cpu_baseline(m, n, k, *, budget_s: float = 12.0, max_reps: int = 30):
+    """The reference's CPU path (torch addmm + erf GELU, fp32) on the host cores."""
+    from oracle.fused_linear import reference_cpu
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(m, k, generator=g) * k ** -0.25
+    w = torch.randn(n, k, generator=g) * k ** -0.25
+    bias = torch.rand(n, generator=g) * 0.2 - 0.1
+    reference_cpu(a, w.t(), bias, "gelu")
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < max_reps and (len(samples) < 3 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        reference_cpu(a, w.t(), bias, "gelu")
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    return {
+        "value": 2 * m * n * k / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"torch.addmm(bias, A, W^T) + F.gelu on the CPU, fp32, M=N=K=4096 (full problem), "
+                  f"median of {len(samples)} runs, {med * 1e3:.1f} ms each",
+        "host_cpu_count": os.cpu_count(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the kernel is single-GPU; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.backends.cuda.matmul.allow_tf32 = False
+    m = n = k = 4096
+    head = gemm_workload("fused_addmm_bias_gelu_erf_fp32_4096", m, n, k, torch.float32,
+                         steps=args.steps, warmup=args.warmup)
+    result = {
+        "metric": "fused linear+bias+GELU TFLOP/s (fp32 M=N=K=4096, B=W^T, erf GELU)",
+        "value": round(head["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0, K**-0.5) operands, U(-0.1,0.1) bias)",
+        "config": {"workload": "fused addmm+bias+GELU(erf), fp32, M=N=K=4096, A row-major, B=W^T strided",
+                   "M": m, "N": n, "K": k, "tile": head["tile"]},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(head["kernel_tflops"], 3),
+            "peak": PEAK_TFLOPS[torch.float32],
+            "unit": "TFLOP/s",
+            "frac": round(head["kernel_tflops"] / PEAK_TFLOPS[torch.float32], 4),
+            "traffic": None,
+            "kernel_us_avg": round(head["kernel_ms_avg"] * 1e3, 2),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(m, n, k)
+    if not args.no_extra:
+        extra = []
+        extra.append(gemm_workload("decoder_mlp_up_bf16_8192x14336x4096_gelu", 8192, 14336, 4096, torch.bfloat16,
+                                   steps=10, warmup=3, bias=False, a_std=1.0, w_std=0.02))
+        extra.append(gemm_workload("decoder_mlp_down_bf16_8192x4096x14336_bias", 8192, 4096, 14336, torch.bfloat16,
+                                   steps=10, warmup=3, act="none", a_std=0.5, w_std=0.02))
+        extra.append(gemm_workload("fused_addmm_bias_gelu_bf16_4096", 4096, 4096, 4096, torch.bfloat16,
+                                   steps=20, warmup=5))
+        from forgeml_amd.neural import TransformerBlock, make_mlp
+
+        torch.manual_seed(0)
+        mlp = make_mlp(512, 2048, 512)
+        torch.manual_seed(1)
+        extra.append(compiled_workload("compiled_mlp_64x512x2048_fp32", mlp, torch.randn(64, 512),
+                                       steps=25, warmup=5))
+        torch.manual_seed(0)
+        block = TransformerBlock(768, 12, 3072).eval()
+        extra.append(compiled_workload("compiled_transformer_block_8x512x768_fp32", block,
+                                       torch.randn(8, 512, 768), steps=10, warmup=3))
+        result["extra"] = extra
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,11 @@
+// fused_gemm_f16.hip — instantiates the f16 fused GEMM kernels of every tile
+// configuration (one translation unit per dtype so they build in parallel).
+#include "gemm_launch.hpp"
+#include "tile_table.hpp"
+
+namespace forgeml {
+#define FORGEML_INSTANTIATE(bm, bn, wm, wn) \
+  template int launch_tile<DT_F16, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
+FORGEML_H16_TILES(FORGEML_INSTANTIATE)
+#undef FORGEML_INSTANTIATE
+}  // namespace forgeml

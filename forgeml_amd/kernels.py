@@ -1,0 +1,266 @@
+"""Kernel boundary: the fused GEMM + bias + activation entry point.
+
+``matmul`` is the drop-in for ForgeML's ``kernels.matmul``
+(src/forgeml/kernels.py:52-116): same signature, same validation order and
+``GraphError`` messages, same ownership rules (the caller owns every buffer;
+``out`` may be a planner slot view; ``out`` must not share storage with an
+input).  Where the reference launches its Triton kernel
+(src/forgeml/kernels.py:206-209 -> src/forgeml/_triton.py:65-93) this calls
+the hand-written gfx950 kernels through the C ABI on the current HIP stream.
+
+Tile configurations are compiled ahead of time, so ``KernelConfig`` names an
+entry of the library's MI355X tile table instead of Triton meta-parameters
+(src/forgeml/kernels.py:12-32).  ``DEFAULT_CONFIG`` selects a tile by shape.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib.resources
+from dataclasses import dataclass, fields
+
+import torch
+
+from forgeml_amd import _native
+from forgeml_amd.ir import Graph, GraphError
+
+
+@dataclass(frozen=True)
+class KernelConfig:
+    """One MI355X tile configuration, or all-None for the shape heuristic.
+
+    block_m x block_n is the output tile of one workgroup, block_k the K
+    elements staged per LDS buffer (128 bytes: 32 fp32 or 64 bf16/fp16),
+    num_waves the 64-lane wavefronts per workgroup and num_stages the LDS
+    buffers in the software pipeline.
+    """
+
+    block_m: int | None = None
+    block_n: int | None = None
+    block_k: int | None = None
+    num_waves: int | None = None
+    num_stages: int | None = None
+
+    @property
+    def is_auto(self) -> bool:
+        return all(getattr(self, f.name) is None for f in fields(self))
+
+
+DEFAULT_CONFIG = KernelConfig()
+
+# The library's tile table, in config-id order (forgeml_amd/csrc/tile_table.hpp).
+# A CPU test checks it against forgeml_hip_config_info.
+_FP32_TILES = ((128, 128, 4), (64, 64, 4), (256, 128, 8))
+_H16_TILES = ((256, 256, 4), (128, 128, 4), (64, 64, 4))
+CANDIDATES: tuple[KernelConfig, ...] = tuple(
+    [KernelConfig(bm, bn, 32, w, 2) for bm, bn, w in _FP32_TILES]
+    + [KernelConfig(bm, bn, 64, w, 2) for bm, bn, w in _H16_TILES]
+)
+_CONFIG_IDS = {cfg: i for i, cfg in enumerate(CANDIDATES)}
+
+_DTYPES = {torch.float16, torch.bfloat16, torch.float32}
+_DTYPE_CODES = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_F16}
+_ACTIVATIONS = ("none", "gelu", "relu")
+GEMM_OPS = ("matmul", "linear", "fused_linear_gelu")
+TARGET_ARCH = "gfx950"
+
+
+def candidates(dtype: torch.dtype) -> tuple[KernelConfig, ...]:
+    """Tile configurations built for ``dtype`` (the autotuner's search space)."""
+    block_k = 32 if dtype == torch.float32 else 64
+    return tuple(c for c in CANDIDATES if c.block_k == block_k)
+
+
+def _device_arch(device: torch.device) -> str:
+    props = torch.cuda.get_device_properties(device)
+    return str(getattr(props, "gcnArchName", "")).split(":")[0]
+
+
+def _gpu_ok(device: torch.device | None = None) -> bool:
+    if not torch.cuda.is_available():
+        return False
+    try:
+        return _device_arch(device or torch.device("cuda", torch.cuda.current_device())) == TARGET_ARCH
+    except (RuntimeError, AssertionError):
+        return False
+
+
+def available() -> bool:
+    """True when a gfx950 GPU is visible and the kernel library loads."""
+    if not _gpu_ok():
+        return False
+    try:
+        _native.load()
+    except _native.NativeLibraryError:
+        return False
+    return True
+
+
+def _check_config(config: KernelConfig, dtype: torch.dtype) -> int:
+    if not isinstance(config, KernelConfig):
+        raise GraphError(f"config must be a KernelConfig, got {type(config).__name__}")
+    if config.is_auto:
+        return _native.CONFIG_AUTO
+    built = candidates(dtype)
+    if config not in built:
+        raise GraphError(f"config {config} is not a built MI355X tile for {dtype}; choose one of {list(built)}")
+    return _CONFIG_IDS[config]
+
+
+def config_id(config: KernelConfig, dtype: torch.dtype) -> int:
+    """Library config id of ``config`` for ``dtype`` (-1 = shape heuristic)."""
+    return _check_config(config, dtype)
+
+
+def resolve_config(m: int, n: int, k: int, dtype: torch.dtype, config: KernelConfig = DEFAULT_CONFIG) -> KernelConfig:
+    """The concrete tile ``config`` runs with for an (m, n, k) GEMM."""
+    cid = _check_config(config, dtype)
+    if cid == _native.CONFIG_AUTO:
+        cid = _native.load().forgeml_hip_select_config(m, n, k, _DTYPE_CODES[dtype])
+        if cid < 0:
+            raise GraphError(f"select_config failed: {_native.last_error()}")
+    return CANDIDATES[cid]
+
+
+def _act_code(activation: str, approximate: str) -> int:
+    if activation == "gelu":
+        return _native.ACT_GELU_ERF if approximate == "none" else _native.ACT_GELU_TANH
+    if activation == "relu":
+        return _native.ACT_RELU
+    return _native.ACT_NONE
+
+
+def launch(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    bias: torch.Tensor | None,
+    out: torch.Tensor,
+    *,
+    act: int,
+    config_id: int,
+    workspace: torch.Tensor | None = None,
+    stream: int | None = None,
+) -> torch.Tensor:
+    """Unchecked launch of the fused kernel (arguments already validated)."""
+    lib = _native.load()
+    m, k = a.shape
+    n = b.shape[1]
+    dtype = _DTYPE_CODES[a.dtype]
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    if stream is None:
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+    rc = lib.forgeml_hip_gemm(
+        a.data_ptr(), a.stride(0), a.stride(1),
+        b.data_ptr(), b.stride(0), b.stride(1),
+        None if bias is None else bias.data_ptr(), 0 if bias is None else bias.stride(0),
+        out.data_ptr(), m, n, k, dtype, act, config_id, ws_ptr, ws_bytes, ctypes.c_void_p(stream),
+    )
+    if rc != _native.OK:
+        msg = f"forgeml_hip_gemm failed ({rc}): {_native.last_error()}"
+        raise GraphError(msg) if rc in (_native.EINVAL, _native.ECONFIG) else RuntimeError(msg)
+    return out
+
+
+def workspace_for(m: int, n: int, k: int, dtype: torch.dtype, cid: int, device: torch.device) -> torch.Tensor | None:
+    nbytes = _native.load().forgeml_hip_gemm_workspace_size(m, n, k, _DTYPE_CODES[dtype], cid)
+    if nbytes < 0:
+        raise GraphError(f"workspace_size failed: {_native.last_error()}")
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def matmul(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    *,
+    activation: str = "none",
+    approximate: str = "none",
+    config: KernelConfig = DEFAULT_CONFIG,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """out = act(rnd(rnd(a @ b) + bias)) on the gfx950 kernels.
+
+    ``activation`` is "none", "gelu" (``approximate`` "none" = erf, "tanh")
+    or "relu" (clamp_min(x, 0), the executor's relu slot writer fused into
+    the epilogue).  Launches on ``torch.cuda.current_stream()`` of ``a``'s
+    device and returns ``out`` (allocated when None).
+    """
+    if not torch.cuda.is_available():
+        raise GraphError("hip matmul requires a ROCm GPU visible to torch (torch.cuda)")
+    _native.load()
+    if not isinstance(a, torch.Tensor) or not isinstance(b, torch.Tensor):
+        raise GraphError("matmul inputs must be tensors")
+    if not a.is_cuda or not b.is_cuda or a.device != b.device:
+        raise GraphError("matmul inputs must be GPU tensors on the same device")
+    if a.dtype not in _DTYPES or a.dtype != b.dtype:
+        raise GraphError(f"matmul dtype {a.dtype} not supported or mismatched")
+    if a.dim() != 2 or b.dim() != 2:
+        raise GraphError("matmul requires rank-2 inputs")
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2 or m <= 0 or n <= 0 or k <= 0:
+        raise GraphError(f"matmul incompatible shapes {a.shape} x {b.shape}")
+    if activation not in _ACTIVATIONS:
+        raise GraphError(f"activation must be one of {_ACTIVATIONS}, got {activation!r}")
+    if approximate not in ("none", "tanh"):
+        raise GraphError(f"approximate must be 'none' or 'tanh', got {approximate!r}")
+    if activation != "gelu" and approximate != "none":
+        raise GraphError("approximate only applies when activation='gelu'")
+    if bias is not None and (
+        not isinstance(bias, torch.Tensor)
+        or not bias.is_cuda
+        or bias.device != a.device
+        or bias.dtype != a.dtype
+        or bias.dim() != 1
+        or bias.shape[0] != n
+    ):
+        raise GraphError("bias must be a 1-D GPU tensor of output width matching dtype/device")
+    cid = _check_config(config, a.dtype)
+    if _device_arch(a.device) != TARGET_ARCH:
+        raise GraphError(f"the HIP kernels are built for {TARGET_ARCH}; device {a.device} is {_device_arch(a.device)}")
+    if out is None:
+        out = torch.empty((m, n), dtype=a.dtype, device=a.device)
+    else:
+        if (
+            not isinstance(out, torch.Tensor)
+            or tuple(out.shape) != (m, n)
+            or out.dtype != a.dtype
+            or out.device != a.device
+            or not out.is_contiguous()
+        ):
+            raise GraphError("out must be a contiguous tensor of shape (M, N) matching dtype/device")
+        out_ptr = out.untyped_storage().data_ptr()
+        for src in (a, b, bias):
+            if src is not None and src.untyped_storage().data_ptr() == out_ptr:
+                raise GraphError("out must not share storage with inputs")
+    with torch.cuda.device(a.device):
+        ws = workspace_for(m, n, k, a.dtype, cid, a.device)
+        return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws)
+
+
+def select_kernels(graph: Graph, backend: str) -> dict[str, str]:
+    """Per-node backend plan: "hip" for GEMM nodes on a gfx950 GPU, else "torch"."""
+    if backend == "torch":
+        return {n.name: "torch" for n in graph.nodes}
+    if backend not in ("auto", "hip"):
+        raise GraphError(f"unsupported backend {backend!r}; expected 'torch', 'hip', or 'auto'")
+    can = available()
+    specs = graph.specs()
+    if backend == "hip":
+        if not can:
+            raise GraphError("backend 'hip' requires a gfx950 GPU and the built kernel library")
+        if not all(torch.device(s.device).type == "cuda" for s in graph.inputs.values()):
+            raise GraphError("backend 'hip' requires GPU graph inputs")
+    plan = {}
+    for node in graph.nodes:
+        on_gpu = all(torch.device(specs[i].device).type == "cuda" for i in node.inputs)
+        if can and node.op in GEMM_OPS and node.spec.dtype in _DTYPES and (backend == "hip" or on_gpu):
+            plan[node.name] = "hip"
+        else:
+            plan[node.name] = "torch"
+    return plan
+
+
+def kernel_source() -> str:
+    """Source text of the HIP kernels (the reference returns its Triton source)."""
+    return importlib.resources.files("forgeml_amd").joinpath("csrc", "gemm_kernels.hpp").read_text()

@@ -1,0 +1,123 @@
+/*
+ * forgeml_hip.h — C ABI of the MI355X (gfx950) fused linear kernels.
+ *
+ * The library computes, on one HIP stream,
+ *
+ *     C[M,N] = act( rnd( rnd( sum_k A[m,k] * B[k,n] ) + bias[n] ) )
+ *
+ * with fp32 accumulation on MFMA, where rnd() rounds to the output dtype
+ * (identity for fp32), the bias add is optional and act is none, exact-erf
+ * GELU, tanh GELU or clamp_min(x, 0).  A and B may have any element strides;
+ * C is contiguous with row stride N.  This is the contract of ForgeML's
+ * Triton `_matmul_kernel` (src/forgeml/_triton.py:6-62), whose launcher
+ * `launch(a, b, bias, out, approximate, config, activation)`
+ * (src/forgeml/_triton.py:65-93) is what `forgeml_hip_gemm` replaces.
+ *
+ * Ownership: every pointer belongs to the caller.  The library never
+ * allocates or frees device memory.  Kernels that split the K reduction use
+ * the caller's workspace (see forgeml_hip_gemm_workspace_size).
+ *
+ * Threading: all entry points are reentrant.  Errors are reported through the
+ * return code and a thread-local message (forgeml_hip_last_error).
+ */
+#ifndef FORGEML_HIP_H
+#define FORGEML_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the reference accepts fp16, bf16 and fp32: kernels.py:29-32). */
+#define FORGEML_DTYPE_F32 0
+#define FORGEML_DTYPE_BF16 1
+#define FORGEML_DTYPE_F16 2
+
+/* Epilogue activations.  1 and 2 are the reference's ACT codes
+ * (src/forgeml/_triton.py:47-57, :70); 3 is the executor's relu slot writer,
+ * clamp_min(x, 0) (src/forgeml/compiler.py:103-104), fused here. */
+#define FORGEML_ACT_NONE 0
+#define FORGEML_ACT_GELU_ERF 1
+#define FORGEML_ACT_GELU_TANH 2
+#define FORGEML_ACT_RELU 3
+
+/* Return codes. */
+#define FORGEML_OK 0
+#define FORGEML_EINVAL (-1)   /* bad argument: shape, stride, dtype, act, pointer */
+#define FORGEML_ECONFIG (-2)  /* config id unknown or not built for this dtype */
+#define FORGEML_EHIP (-3)     /* the HIP runtime reported an error */
+#define FORGEML_EWORKSPACE (-4) /* workspace missing or too small */
+
+/* Config id meaning "choose by shape" (the reference's DEFAULT_CONFIG,
+ * src/forgeml/kernels.py:13-21, is a fixed tile; here the default is a
+ * shape heuristic over the MI355X tile table). */
+#define FORGEML_CONFIG_AUTO (-1)
+
+/* Fields returned by forgeml_hip_config_info, in order. */
+#define FORGEML_CONFIG_INFO_FIELDS 8
+/* [0] dtype class: 0 = fp32, 1 = 16-bit (bf16 and fp16)
+ * [1] block_m   [2] block_n   [3] block_k (elements per LDS stage)
+ * [4] waves per workgroup     [5] LDS stages
+ * [6] split_k (1 = none; >1 = K split over workgroups, needs a workspace)
+ * [7] LDS bytes per workgroup */
+
+/*
+ * Fused GEMM + bias + activation.  Replaces `launch` in
+ * src/forgeml/_triton.py:65-93 (called from kernels.matmul,
+ * src/forgeml/kernels.py:206-209).
+ *
+ *   a        [M,K] element (m,k) at a + (m*sam + k*sak) elements
+ *   b        [K,N] element (k,n) at b + (k*sbk + n*sbn) elements
+ *   bias     [N] element n at bias + n*sbi; NULL for no bias
+ *   c        [M,N] contiguous, element (m,n) at c + m*N + n
+ *   dtype    FORGEML_DTYPE_*; a, b, bias and c share it
+ *   act      FORGEML_ACT_*
+ *   config_id  index into the tile table, or FORGEML_CONFIG_AUTO
+ *   workspace, workspace_bytes  device scratch for split-K configs
+ *            (may be NULL/0 when forgeml_hip_gemm_workspace_size is 0)
+ *   stream   hipStream_t to launch on (NULL = the null stream)
+ *
+ * Returns FORGEML_OK or a negative FORGEML_E* code.  The launch is
+ * asynchronous; errors raised while the kernel runs surface on the stream.
+ */
+int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
+                     const void* b, int64_t sbk, int64_t sbn,
+                     const void* bias, int64_t sbi,
+                     void* c, int64_t m, int64_t n, int64_t k,
+                     int32_t dtype, int32_t act, int32_t config_id,
+                     void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/* Bytes of workspace forgeml_hip_gemm needs for this shape and config
+ * (0 for configs that do not split K).  Negative on bad arguments.
+ * No reference counterpart: the reference has no split-K kernel. */
+int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k,
+                                        int32_t dtype, int32_t config_id);
+
+/* The config id FORGEML_CONFIG_AUTO resolves to for this shape.
+ * Counterpart of DEFAULT_CONFIG (src/forgeml/kernels.py:21). */
+int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype);
+
+/* Number of entries in the tile table.  Counterpart of
+ * len(CANDIDATES) (src/forgeml/kernels.py:22-27). */
+int forgeml_hip_num_configs(void);
+
+/* Writes FORGEML_CONFIG_INFO_FIELDS int32 values describing config `id`.
+ * Counterpart of the KernelConfig fields (src/forgeml/kernels.py:12-18). */
+int forgeml_hip_config_info(int32_t id, int32_t* out);
+
+/* Thread-local text of the last error on this thread ("" if none).
+ * The reference raises Python exceptions instead (kernels.py:62-112). */
+const char* forgeml_hip_last_error(void);
+
+/* ABI version of this header; bumped on any signature change. */
+int forgeml_hip_abi_version(void);
+
+#define FORGEML_HIP_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGEML_HIP_H */

@@ -1,0 +1,230 @@
+"""GPU parity of the gfx950 fused GEMM kernels against ForgeML's CPU path.
+
+Every case compares ``forgeml_amd.kernels.matmul`` (C ABI -> HIP kernel)
+with ``oracle.fused_linear.reference_cpu`` (torch addmm/mm + GELU on the
+CPU, src/forgeml/ops.py:28-53) on the same seeded inputs, under the gate of
+``oracle.fused_linear.tolerance``: fp32 rtol 1e-4 / atol 1e-5*sqrt(K), bf16
+rtol 2e-2 / atol 5e-2, fp16 1e-2 / 1e-2; non-finite output always fails.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from forgeml_amd import kernels
+from forgeml_amd.ir import GraphError
+from oracle.fused_linear import kernel_contract, reference_cpu, tolerance
+from tests.cases import case_seed, gemm_inputs, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*parts):
+    print("case:", *parts, flush=True)
+
+
+def _gate(got: torch.Tensor, expected: torch.Tensor, k: int, what: str):
+    got = got.detach().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite output"
+    rtol, atol = tolerance(expected.dtype, k)
+    torch.testing.assert_close(got.float(), expected.float(), rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
+
+
+# -- the reference's own GPU kernel tests (tests/test_kernels.py:101-161) ------
+
+_DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+@pytest.mark.parametrize("m,n,k", [(1, 17, 9), (31, 65, 33), (64, 64, 64)])
+def test_matmul_small_shapes(gpu, dtype, m, n, k):
+    g = torch.Generator().manual_seed(case_seed("small", m, n, k, dtype))
+    a = torch.randn(m, k, generator=g).to(dtype)
+    b = torch.randn(k, n, generator=g).to(dtype)
+    _say("matmul", m, n, k, dtype)
+    got = kernels.matmul(a.to(gpu), b.to(gpu))
+    # tests/test_kernels.py:110 expects torch.matmul(a.float(), b.float()).to(dtype)
+    expected = torch.matmul(a.float(), b.float()).to(dtype)
+    ref_rtol, ref_atol = {torch.float32: (1e-4, 1e-4), torch.float16: (1e-2, 1e-2), torch.bfloat16: (5e-2, 5e-2)}[dtype]
+    torch.testing.assert_close(got.cpu().float(), expected.float(), rtol=ref_rtol, atol=ref_atol)
+    _gate(got, reference_cpu(a, b), k, "vs CPU path")
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_bias_gelu(gpu, dtype, approximate):
+    g = torch.Generator().manual_seed(case_seed("bias_gelu", dtype, approximate))
+    a = torch.randn(16, 32, generator=g).to(dtype)
+    b = torch.randn(32, 24, generator=g).to(dtype)
+    bias = torch.randn(24, generator=g).to(dtype)
+    _say("bias_gelu", dtype, approximate)
+    got = kernels.matmul(a.to(gpu), b.to(gpu), bias.to(gpu), activation="gelu", approximate=approximate).cpu()
+    # tests/test_kernels.py:124-126: gelu((a.float() @ b.float()).to(dtype) + bias)
+    expected = torch.nn.functional.gelu((a.float() @ b.float()).to(dtype) + bias, approximate=approximate)
+    ref_rtol, ref_atol = {torch.float32: (1e-4, 1e-4), torch.float16: (1e-2, 1e-2), torch.bfloat16: (5e-2, 5e-2)}[dtype]
+    torch.testing.assert_close(got.float(), expected.float(), rtol=ref_rtol, atol=ref_atol)
+    _gate(got, reference_cpu(a, b, bias, "gelu", approximate), 32, "vs CPU path")
+    # The kernel's epilogue order is exactly the reference kernel's contract.
+    contract = kernel_contract(a, b, bias, "gelu", approximate)
+    torch.testing.assert_close(got.float(), contract.float(), rtol=tolerance(dtype, 32)[0], atol=1e-5 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_strided_bias(gpu, approximate):
+    g = torch.Generator().manual_seed(case_seed("strided_bias", approximate))
+    a = torch.randn(16, 32, generator=g)
+    b = torch.randn(32, 24, generator=g)
+    bias_full = torch.randn(48, generator=g)
+    _say("strided_bias", approximate)
+    got = kernels.matmul(a.to(gpu), b.to(gpu), bias_full.to(gpu)[::2], activation="gelu", approximate=approximate)
+    _gate(got, reference_cpu(a, b, bias_full[::2], "gelu", approximate), 32, "strided bias")
+
+
+def test_noncontiguous_inputs(gpu):
+    g = torch.Generator().manual_seed(case_seed("noncontig"))
+    a = torch.randn(32, 16, generator=g)
+    b = torch.randn(24, 32, generator=g)
+    _say("noncontiguous")
+    got = kernels.matmul(a.to(gpu).t(), b.to(gpu).t())
+    _gate(got, reference_cpu(a.t(), b.t()), 32, "transposed A and B")
+
+
+def test_out_buffer_and_overlap_reject(gpu):
+    a = torch.randn(16, 16, device=gpu)
+    b = torch.randn(16, 16, device=gpu)
+    out = torch.empty(16, 16, device=gpu)
+    _say("out buffer")
+    got = kernels.matmul(a, b, out=out)
+    assert got.data_ptr() == out.data_ptr()
+    _gate(out, reference_cpu(a.cpu(), b.cpu()), 16, "out=")
+    with pytest.raises(GraphError, match="storage"):
+        kernels.matmul(a, b, out=a)
+
+
+def test_relu_epilogue(gpu):
+    a, b, bias = gemm_inputs(96, 200, 136, torch.float32, seed=case_seed("relu"))
+    _say("relu epilogue")
+    got = kernels.matmul(to_gpu(a, gpu), to_gpu(b, gpu), bias.to(gpu), activation="relu")
+    _gate(got, reference_cpu(a, b, bias, "relu"), 136, "relu")
+
+
+# -- ragged and edge-masked sweep (M x N x K x dtype, +-bias, +-GELU) ----------
+
+_SWEEP_M = [1, 7, 33, 257, 1000]
+_SWEEP_N = [768, 3072, 3000]
+_SWEEP_K = [768, 1024, 1531]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("k", _SWEEP_K)
+@pytest.mark.parametrize("n", _SWEEP_N)
+@pytest.mark.parametrize("m", _SWEEP_M)
+def test_ragged_sweep(gpu, m, n, k, dtype):
+    seed = case_seed("sweep", m, n, k, dtype)
+    a, b_nt, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout="nt")
+    a_d = a.to(gpu)
+    layouts = {"nt": to_gpu(b_nt, gpu), "nn": b_nt.contiguous().to(gpu)}
+    bias_d = bias.to(gpu)
+    for with_bias in (False, True):
+        for activation in ("none", "gelu"):
+            expected = reference_cpu(a, b_nt, bias if with_bias else None, activation)
+            for name, b_d in layouts.items():
+                what = f"M={m} N={n} K={k} {dtype} B={name} bias={with_bias} act={activation} seed={seed}"
+                _say(what)
+                got = kernels.matmul(a_d, b_d, bias_d if with_bias else None, activation=activation)
+                _gate(got, expected, k, what)
+
+
+# -- every tile configuration x operand layout ---------------------------------
+
+def _layouts(m, n, k, dtype, seed):
+    """(name, make_a, make_b) covering the K-, MN-contiguous and generic load paths.
+
+    The makers build the operand on a device so that strided views keep
+    their strides there.
+    """
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(m, k, generator=g) * k ** -0.25).to(dtype)
+    w = (torch.randn(n, k, generator=g) * k ** -0.25).to(dtype)
+    a_pad = torch.zeros(m, 2 * k, dtype=dtype)
+    a_pad[:, ::2] = a
+    row_major_a = lambda dev: a.to(dev)                          # stride (K, 1)
+    col_major_a = lambda dev: a.t().contiguous().to(dev).t()     # stride (1, M)
+    strided_a = lambda dev: a_pad.to(dev)[:, ::2]                # stride (2K, 2): generic path
+    b_nt = lambda dev: w.to(dev).t()                             # B = W^T, stride (1, K)
+    b_kn = lambda dev: w.t().contiguous().to(dev)                # B [K,N], stride (N, 1)
+    return a, w, [
+        ("K,K", row_major_a, b_nt),
+        ("K,MN", row_major_a, b_kn),
+        ("MN,K", col_major_a, b_nt),
+        ("MN,MN", col_major_a, b_kn),
+        ("G,G", strided_a, b_nt),
+    ]
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_every_config_and_layout(gpu, dtype):
+    m, n, k = 392, 328, 520  # multiples of 8, not of any tile: edge tiles everywhere
+    seed = case_seed("configs", dtype)
+    a, w, layouts = _layouts(m, n, k, dtype, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    bias = (torch.rand(n, generator=g) * 0.2 - 0.1).to(dtype)
+    expected = reference_cpu(a, w.t(), bias, "gelu")
+    for config in kernels.candidates(dtype):
+        for name, make_a, make_b in layouts:
+            what = f"{dtype} config={config} layout={name} seed={seed}"
+            _say(what)
+            a_d, b_d = make_a(gpu), make_b(gpu)
+            got = kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
+            _gate(got, expected, k, what)
+
+
+def test_deterministic(gpu):
+    a, b, bias = gemm_inputs(512, 768, 1024, torch.bfloat16, seed=case_seed("det"))
+    a, b, bias = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+    _say("determinism")
+    first = kernels.matmul(a, b, bias, activation="gelu")
+    second = kernels.matmul(a, b, bias, activation="gelu")
+    assert torch.equal(first, second)
+
+
+# -- full-size configurations: sampled rows are exact parity cases -------------
+
+def _row_sample(m: int, count: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randperm(m, generator=g)[: count - 2]
+    return torch.cat([torch.tensor([0, m - 1]), rows]).sort().values
+
+
+def test_fp32_4096_cube_nt(gpu):
+    """fp32 M=N=K=4096, B = W^T (nn.Linear weight), bias, exact-erf GELU."""
+    m = n = k = 4096
+    seed = case_seed("c2", m)
+    a, b, bias = gemm_inputs(m, n, k, torch.float32, seed=seed, b_layout="nt")
+    _say("fp32 4096^3 NT bias+gelu", seed)
+    got = kernels.matmul(to_gpu(a, gpu), to_gpu(b, gpu), bias.to(gpu), activation="gelu").cpu()
+    assert torch.isfinite(got).all()
+    rows = _row_sample(m, 64, seed)
+    expected = reference_cpu(a[rows], b, bias, "gelu")
+    _gate(got[rows], expected, k, "fp32 4096^3 sampled rows")
+
+
+def test_bf16_decoder_mlp(gpu):
+    """bf16 M=8192: [4096->14336]+GELU, then [14336->4096]+bias (fp32 accumulate)."""
+    m, d, f = 8192, 4096, 14336
+    seed = case_seed("c5", m, d, f)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(f, d, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(d, f, generator=g) * 0.02).to(torch.bfloat16)
+    b2 = (torch.rand(d, generator=g) * 0.2 - 0.1).to(torch.bfloat16)
+    _say("bf16 decoder MLP", seed)
+    h = kernels.matmul(x.to(gpu), to_gpu(w1.t(), gpu), activation="gelu")
+    y = kernels.matmul(h, to_gpu(w2.t(), gpu), b2.to(gpu))
+    rows = _row_sample(m, 32, seed)
+    h_rows = h[rows.to(gpu)].cpu()
+    _gate(h_rows, reference_cpu(x[rows], w1.t(), None, "gelu"), d, "up GEMM sampled rows")
+    # The down GEMM is checked on the kernel's own H rows (same inputs).
+    _gate(y[rows.to(gpu)], reference_cpu(h_rows, w2.t(), b2), f, "down GEMM sampled rows")
+    assert torch.isfinite(y).all()
