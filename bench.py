@@ -32,6 +32,7 @@ import torch  # noqa: E402
 
 PEAK_TFLOPS = {torch.float32: 157.3, torch.bfloat16: 2516.6, torch.float16: 2516.6}
 HBM_GBPS = 8000.0
+COPY_BYTES = 256 * 1024 * 1024  # --calibrate-copy: bytes read and bytes written by the copy
 DTYPE_NAMES = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
 
 
@@ -152,6 +153,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -161,6 +164,13 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.calibrate_copy:
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     m = n = k = 4096
     head = gemm_workload("fused_addmm_bias_gelu_erf_fp32_4096", m, n, k, torch.float32,
                          steps=args.steps, warmup=args.warmup)
