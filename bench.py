@@ -146,6 +146,18 @@ def cpu_baseline(m, n, k, *, budget_s: float = 12.0, max_reps: int = 30):
     }
 
 
+def _measured_traffic(key: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs, if
+    they were taken for this exact kernel tile; None otherwise."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    try:
+        table = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = table.get(key)
+    return None if entry is None else entry["traffic_bytes"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,7 +207,8 @@ def main() -> int:
             "peak": PEAK_TFLOPS[torch.float32],
             "unit": "TFLOP/s",
             "frac": round(head["kernel_tflops"] / PEAK_TFLOPS[torch.float32], 4),
-            "traffic": None,
+            "traffic": _measured_traffic(f"fp32 {m}x{n}x{k} B=W^T tile={head['tile'][0]}x{head['tile'][1]}x"
+                                         f"{head['tile'][2]} waves={head['tile'][3]}"),
             "kernel_us_avg": round(head["kernel_ms_avg"] * 1e3, 2),
         },
     }
