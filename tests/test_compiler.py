@@ -1,0 +1,144 @@
+"""Executor behaviour (src/forgeml/compiler.py) on the CPU, including the GPU
+dispatch path driven through a fake kernel (the reference's strategy,
+tests/test_compiler.py:180-214)."""
+
+import json
+
+import pytest
+import torch
+from torch import nn
+
+import forgeml_amd
+from forgeml_amd import kernels
+from forgeml_amd.frontend import from_torch
+from forgeml_amd.ir import GraphBuilder, GraphError, TensorSpec
+
+
+def make_mlp():
+    torch.manual_seed(0)
+    return nn.Sequential(nn.Linear(8, 16), nn.GELU(approximate="tanh"), nn.Linear(16, 4)).eval()
+
+
+def spec(*shape):
+    return TensorSpec(tuple(shape), torch.float32, "cpu")
+
+
+def test_mlp_parity_and_fusion():
+    m = make_mlp()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(m, (x,))
+    assert [n.op for n in c.graph.nodes] == ["fused_linear_gelu", "linear"]
+    torch.testing.assert_close(c(x), m(x))
+
+
+def test_backend_rejection_and_hip_requires_gpu():
+    with pytest.raises(GraphError, match="backend"):
+        forgeml_amd.compile(make_mlp(), (torch.randn(4, 8),), backend="triton")
+    if not kernels.available():
+        with pytest.raises(GraphError, match="hip"):
+            forgeml_amd.compile(make_mlp(), (torch.randn(4, 8),), backend="hip")
+        c = forgeml_amd.compile(make_mlp(), (torch.randn(4, 8),), backend="auto")
+        assert set(c.kernel_plan.values()) == {"torch"}
+
+
+def test_outputs_independent_across_calls():
+    m = make_mlp()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(m, (x,))
+    out1 = c(x)
+    keep = out1.clone()
+    out2 = c(x + 1.0)
+    torch.testing.assert_close(out1, keep)
+    assert out1.data_ptr() != out2.data_ptr()
+
+
+def test_explain_is_json_and_consistent():
+    c = forgeml_amd.compile(make_mlp(), (torch.randn(4, 8),))
+    e = c.explain()
+    assert "fused_linear_gelu" in json.dumps(e)
+    assert e["optimized_nodes"] <= e["original_nodes"]
+    assert e["memory_plan"]["planned_bytes"] <= e["memory_plan"]["naive_bytes"]
+    assert e["optimization_delta"]["nodes"] == e["original_nodes"] - e["optimized_nodes"]
+
+
+def test_internal_linear_writes_into_its_slot():
+    m = nn.Sequential(nn.Linear(8, 16), nn.ReLU(), nn.Linear(16, 4, bias=False)).eval()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(m, (x,), optimize=False)
+    first = c.graph.nodes[0].name
+    assert first in c.memory_plan.allocations
+    torch.testing.assert_close(c(x), m(x))
+
+
+def test_view_and_output_alias_rules():
+    b = GraphBuilder({"x": spec(4)})
+    b.add("a", "relu", ("x",))
+    b.add("b", "reshape", ("a",), shape=(2, 2))
+    b.add("c", "relu", ("a",))
+    b.constant("two", torch.full((4,), 2.0))
+    b.add("d", "mul", ("c", "two"))
+    b.add("out", "relu", ("d",))
+    c = forgeml_amd.compile(b.finish(("b", "out")), optimize=False)
+    assert c.memory_plan.allocations["d"].slot == c.memory_plan.allocations["a"].slot
+    x = torch.randn(4)
+    out_b, out_d = c(x)
+    torch.testing.assert_close(out_b, torch.relu(x).reshape(2, 2))
+    torch.testing.assert_close(out_d, torch.relu(torch.relu(x) * 2))
+
+
+def test_constants_are_snapshotted():
+    b = GraphBuilder({"x": spec(2)})
+    b.constant("c", torch.ones(2))
+    b.add("y", "add", ("x", "c"))
+    g = b.finish(("y",))
+    c = forgeml_amd.compile(g, optimize=False)
+    g.constants["c"].fill_(99.0)
+    torch.testing.assert_close(c(torch.zeros(2)), torch.ones(2))
+
+
+def test_input_guards():
+    c = forgeml_amd.compile(make_mlp(), (torch.randn(4, 8),))
+    with pytest.raises(GraphError, match="shape"):
+        c(torch.randn(5, 8))
+    with pytest.raises(GraphError, match="dtype"):
+        c(torch.randn(4, 8, dtype=torch.float64))
+    with pytest.raises(GraphError, match="expected 1 inputs"):
+        c()
+
+
+def _fake_matmul(seen):
+    def fake(a, b, bias=None, *, activation="none", approximate="none", config=None, out=None):
+        seen.append((activation, approximate, bias is not None, out is not None))
+        value = a @ b + (bias if bias is not None else 0)
+        if activation == "gelu":
+            value = torch.nn.functional.gelu(value, approximate=approximate)
+        elif activation == "relu":
+            value = torch.clamp_min(value, 0)
+        return value if out is None else out.copy_(value)
+    return fake
+
+
+def test_gpu_dispatch_path_with_fake_kernel(monkeypatch):
+    seen = []
+    monkeypatch.setattr(kernels, "matmul", _fake_matmul(seen))
+    model = make_mlp()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(model, (x,))
+    c.kernel_plan = {n.name: "hip" for n in c.graph.nodes}  # rebuilds the step closures
+    torch.testing.assert_close(c(x), model(x))
+    # the internal fused node writes into its slot (out given), the output gets a fresh tensor
+    assert seen == [("gelu", "tanh", True, True), ("none", "none", True, False)]
+
+
+def test_hip_plan_on_view_op_is_rejected():
+    b = GraphBuilder({"x": spec(2, 4)})
+    b.add("r", "reshape", ("x",), shape=(8,))
+    c = forgeml_amd.compile(b.finish(("r",)), optimize=False)
+    with pytest.raises(GraphError, match="no hip kernel"):
+        c.kernel_plan = {"r": "hip"}
+
+
+def test_explicit_graph_compiles():
+    m = make_mlp()
+    x = torch.randn(4, 8)
+    torch.testing.assert_close(forgeml_amd.compile(from_torch(m, (x,)))(x), m(x))

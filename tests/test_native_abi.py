@@ -1,0 +1,78 @@
+"""The C ABI library: it loads without a GPU, exports every symbol the header
+declares, and its tile table agrees with the Python KernelConfig table.
+No kernel is launched here."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from forgeml_amd import _native, kernels
+from forgeml_amd.ir import GraphError
+
+
+def _declared_symbols() -> list[str]:
+    text = _native.HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(forgeml_hip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert _declared_symbols() == sorted(_native.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in _declared_symbols():
+        assert getattr(lib, name, None) is not None, name
+    assert lib.forgeml_hip_abi_version() == _native.ABI_VERSION
+    assert len(_native.hip_runtimes_mapped()) <= 1
+
+
+def test_config_table_matches_python_candidates():
+    table = _native.config_table()
+    assert len(table) == len(kernels.CANDIDATES)
+    for info, cfg in zip(table, kernels.CANDIDATES):
+        dclass, bm, bn, bk, waves, stages, split, lds = info
+        assert (bm, bn, bk, waves, stages) == (cfg.block_m, cfg.block_n, cfg.block_k, cfg.num_waves, cfg.num_stages)
+        assert dclass == (0 if cfg.block_k == 32 else 1) and split == 1
+        assert lds == 2 * (bm + bn) * 128 and lds <= 160 * 1024
+
+
+def test_host_side_errors_without_launching():
+    lib = _native.load()
+    assert lib.forgeml_hip_select_config(0, 4, 4, _native.DTYPE_F32) == _native.EINVAL
+    assert lib.forgeml_hip_select_config(4, 4, 4, 7) == _native.EINVAL
+    assert lib.forgeml_hip_gemm_workspace_size(4, 4, 4, _native.DTYPE_F32, 99) == _native.ECONFIG
+    rc = lib.forgeml_hip_gemm(None, 0, 0, None, 0, 0, None, 0, None, 4, 4, 4, 0, 0, -1, None, 0, None)
+    assert rc == _native.EINVAL and "non-NULL" in _native.last_error()
+    dummy = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    rc = lib.forgeml_hip_gemm(dummy, 4, 1, dummy, 4, 1, None, 0, dummy, 4, 4, 4, _native.DTYPE_BF16, 0, 0,
+                              None, 0, None)
+    assert rc == _native.ECONFIG and "not built for dtype" in _native.last_error()
+    rc = lib.forgeml_hip_gemm(dummy, 4, 1, dummy, 4, 1, None, 0, dummy, 4, 4, 4, 0, 9, -1, None, 0, None)
+    assert rc == _native.EINVAL and "activation" in _native.last_error()
+    rc = lib.forgeml_hip_gemm(dummy, -4, 1, dummy, 4, 1, None, 0, dummy, 4, 4, 4, 0, 0, -1, None, 0, None)
+    assert rc == _native.EINVAL
+
+
+def test_heuristic_picks_built_tiles():
+    lib = _native.load()
+    for dtype, code in ((torch.float32, _native.DTYPE_F32), (torch.bfloat16, _native.DTYPE_BF16)):
+        for m, n, k in ((1, 768, 768), (64, 2048, 512), (4096, 4096, 4096), (8192, 14336, 4096)):
+            cid = lib.forgeml_hip_select_config(m, n, k, code)
+            assert kernels.CANDIDATES[cid] in kernels.candidates(dtype)
+
+
+def test_matmul_boundary_validation_on_cpu():
+    a = torch.randn(4, 4)
+    if not torch.cuda.is_available():
+        with pytest.raises(GraphError, match="GPU"):
+            kernels.matmul(a, a)
+    with pytest.raises(GraphError):
+        kernels._check_config(kernels.KernelConfig(block_m=8), torch.float32)
+    with pytest.raises(GraphError):
+        kernels._check_config(kernels.candidates(torch.bfloat16)[0], torch.float32)
+    assert kernels._check_config(kernels.DEFAULT_CONFIG, torch.float32) == _native.CONFIG_AUTO
+    assert "fused_gemm_kernel" in kernels.kernel_source() and "__global__" in kernels.kernel_source()
