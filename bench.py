@@ -146,6 +146,19 @@ def cpu_baseline(m, n, k, *, budget_s: float = 12.0, max_reps: int = 30):
     }
 
 
+# Extra GEMM workloads: (M, N, K, dtype) and their options.
+EXTRA_GEMMS = {
+    "decoder_mlp_up_bf16_8192x14336x4096_gelu": (8192, 14336, 4096, torch.bfloat16),
+    "decoder_mlp_down_bf16_8192x4096x14336_bias": (8192, 4096, 14336, torch.bfloat16),
+    "fused_addmm_bias_gelu_bf16_4096": (4096, 4096, 4096, torch.bfloat16),
+}
+EXTRA_KW = {
+    "decoder_mlp_up_bf16_8192x14336x4096_gelu": dict(bias=False, a_std=1.0, w_std=0.02),
+    "decoder_mlp_down_bf16_8192x4096x14336_bias": dict(act="none", a_std=0.5, w_std=0.02),
+    "fused_addmm_bias_gelu_bf16_4096": dict(),
+}
+
+
 def _measured_traffic(key: str):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs, if
     they were taken for this exact kernel tile; None otherwise."""
@@ -165,6 +178,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=sorted(EXTRA_GEMMS), default=None,
+                    help="run one extra GEMM workload only (for profiling) and print its record")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -176,6 +191,10 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.only:
+        print(json.dumps(gemm_workload(args.only, *EXTRA_GEMMS[args.only], steps=args.steps, warmup=args.warmup,
+                                       **EXTRA_KW[args.only])), flush=True)
+        return 0
     if args.calibrate_copy:
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -215,13 +234,8 @@ def main() -> int:
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(m, n, k)
     if not args.no_extra:
-        extra = []
-        extra.append(gemm_workload("decoder_mlp_up_bf16_8192x14336x4096_gelu", 8192, 14336, 4096, torch.bfloat16,
-                                   steps=10, warmup=3, bias=False, a_std=1.0, w_std=0.02))
-        extra.append(gemm_workload("decoder_mlp_down_bf16_8192x4096x14336_bias", 8192, 4096, 14336, torch.bfloat16,
-                                   steps=10, warmup=3, act="none", a_std=0.5, w_std=0.02))
-        extra.append(gemm_workload("fused_addmm_bias_gelu_bf16_4096", 4096, 4096, 4096, torch.bfloat16,
-                                   steps=20, warmup=5))
+        extra = [gemm_workload(name, *EXTRA_GEMMS[name], steps=10, warmup=3, **EXTRA_KW[name])
+                 for name in EXTRA_GEMMS]
         from forgeml_amd.neural import TransformerBlock, make_mlp
 
         torch.manual_seed(0)

@@ -52,11 +52,21 @@ static int esize_of(int dtype) { return dtype == FORGEML_DTYPE_F32 ? 4 : 2; }
 static int dclass_of(int dtype) { return dtype == FORGEML_DTYPE_F32 ? 0 : 1; }
 
 // Load mode of one operand viewed as rows x K with strides (s_mn, s_k).
+// The vector modes address one workgroup's operand panel with 32-bit buffer
+// offsets: rows of the widest tile (256) for K-contiguous operands, all of K
+// for M/N-contiguous ones.
+static constexpr int64_t kMaxPanelRows = 256;
+static constexpr int64_t kMaxBufferBytes = (int64_t)1 << 31;
+
 static int operand_mode(const void* base, int64_t rows, int64_t s_mn, int64_t s_k, int64_t k, int esz) {
   const int vec = 16 / esz;
   const bool aligned = ((uintptr_t)base % 16) == 0;
-  if (aligned && s_k == 1 && s_mn >= 0 && (s_mn * esz) % 16 == 0 && k % vec == 0) return MODE_K;
-  if (aligned && s_mn == 1 && s_k >= 0 && (s_k * esz) % 16 == 0 && rows % vec == 0) return MODE_MN;
+  if (aligned && s_k == 1 && s_mn >= 0 && (s_mn * esz) % 16 == 0 && k % vec == 0 &&
+      (kMaxPanelRows * s_mn + k) * esz < kMaxBufferBytes)
+    return MODE_K;
+  if (aligned && s_mn == 1 && s_k >= 0 && (s_k * esz) % 16 == 0 && rows % vec == 0 &&
+      (k * s_k + kMaxPanelRows) * esz < kMaxBufferBytes)
+    return MODE_MN;
   return MODE_G;
 }
 

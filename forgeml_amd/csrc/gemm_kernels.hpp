@@ -135,88 +135,114 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 // ---------------------------------------------------------------------------
 // Operand stage loaders.  An operand is viewed as ROWS x K with element
 // (r, k) at base + (r*s_mn + k*s_k) elements: A is (M rows, sam, sak), B is
-// (N rows, sbn, sbk).  load(kt) fetches stage kt from global memory into
-// registers, store(lds) writes it into one LDS buffer.
+// (N rows, sbn, sbk).  Each loader fetches one 128-byte-K stage:
+//   issue(kt, stage)  starts the global reads of stage kt;
+//   commit(stage)     finishes writing it into an LDS buffer.
+// Direct loaders (kDirect) DMA global memory straight into LDS in issue()
+// and need only a vmcnt wait before the barrier; the others stage through
+// registers and write LDS in commit().
+//
+// Global reads go through buffer resources: a lane whose element is outside
+// the operand (M/N edge or K tail) gets an offset past the resource's range
+// and the hardware returns zeros, with no branch and no select on the data.
 
-// K contiguous: 16-byte vectors along K, 8 per LDS row.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, uint32_t bytes) {
+  // Word 3 0x00020000: raw (untyped) buffer access on gfx9-family GPUs.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// K contiguous: DMA 16-byte vectors along K straight into LDS.  One
+// buffer_load_dwordx4 ... lds of a wave writes a contiguous 1 KB block (lane
+// L at byte 16*L) = 8 LDS rows; each lane fetches the chunk whose swizzled
+// LDS position is its own slot.
 template <int DT, int ROWS, int NT>
 struct LoaderK {
-  static constexpr int UNITS = ROWS * 8;
-  static constexpr int PER = (UNITS + NT - 1) / NT;
-  const char* base;
-  int64_t ld_bytes;
-  int row0, rows, kbytes;
-  u32x4 v[PER];
+  static constexpr bool kDirect = true;
+  static constexpr int BLOCKS = ROWS / 8;
+  static constexpr int NWAVES = NT / 64;
+  static constexpr int PER = (BLOCKS + NWAVES - 1) / NWAVES;
+  static constexpr int kGlobalLoads = PER, kLdsWrites = 0;  // per thread per stage
+  __amdgpu_buffer_rsrc_t rsrc;
+  int kbytes;
+  uint32_t voff[PER];  // this lane's byte offset in stage 0, or out of range
+  int kchunk[PER];     // byte offset of this lane's chunk within a stage
 
   __device__ void init(const char* b, int64_t s_mn, int64_t /*s_k*/, int r0, int nrows, int k) {
-    base = b;
-    ld_bytes = s_mn * DTraits<DT>::ESZ;
-    row0 = r0;
-    rows = nrows;
+    const int ld_bytes = (int)(s_mn * DTraits<DT>::ESZ);
     kbytes = k * DTraits<DT>::ESZ;
-  }
-  __device__ __forceinline__ void load(int kt) {
+    const int valid_rows = min(ROWS, nrows - r0);
+    const int64_t span = (int64_t)(valid_rows - 1) * ld_bytes + kbytes;
+    rsrc = make_rsrc(b + (int64_t)r0 * s_mn * DTraits<DT>::ESZ, (uint32_t)span);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int q = threadIdx.x + i * NT;
-      const int r = q >> 3, c = q & 7;
-      const int kb = kt * kRowBytes + c * 16;
-      const bool ok = (UNITS % NT == 0 || q < UNITS) && (row0 + r < rows) && (kb < kbytes);
-      u32x4 z = {0u, 0u, 0u, 0u};
-      v[i] = ok ? *(const u32x4*)(base + (int64_t)(row0 + r) * ld_bytes + kb) : z;
+      const int blk = wave + i * NWAVES;
+      const int r = blk * 8 + (lane >> 3);
+      const int c = (lane ^ r ^ (r >> 3)) & 7;  // logical chunk stored at physical slot lane&7
+      kchunk[i] = c * 16;
+      voff[i] = (r < valid_rows && blk < BLOCKS) ? (uint32_t)(r * ld_bytes + c * 16) : kOutOfRange;
     }
   }
-  __device__ __forceinline__ void store(char* lds) {
+  // Stage kt's K offset goes in the scalar offset; lanes past the K tail get
+  // an out-of-range vector offset.
+  __device__ __forceinline__ void issue(int kt, char* stage) {
+    const int wave = threadIdx.x >> 6;
+    const int kbase = kt * kRowBytes;
+    const int klimit = kbytes - kbase;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int q = threadIdx.x + i * NT;
-      if (UNITS % NT == 0 || q < UNITS) {
-        const int r = q >> 3, c = q & 7;
-        *(u32x4*)(lds + lds_off(r, c)) = v[i];
+      const int blk = wave + i * NWAVES;  // uniform per wave
+      if (BLOCKS % NWAVES == 0 || blk < BLOCKS) {
+        const uint32_t off = kchunk[i] < klimit ? voff[i] : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(stage + blk * 1024), 16, off, kbase, 0, 0);
       }
     }
   }
+  __device__ __forceinline__ void commit(char*) {}
 };
 
 // M/N contiguous: each unit is VEC rows x VEC K values, fetched as VEC
-// 16-byte vectors along M/N (one per K value) and transposed in registers
-// into one 16-byte LDS chunk per row.
+// 16-byte vectors along M/N (one per K value) into registers and transposed
+// there into one 16-byte LDS chunk per row.
 template <int DT, int ROWS, int NT>
 struct LoaderMN {
+  static constexpr bool kDirect = false;
   static constexpr int ESZ = DTraits<DT>::ESZ;
   static constexpr int VEC = DTraits<DT>::VEC;
   static constexpr int UM = ROWS / VEC;
   static constexpr int UNITS = UM * 8;
   static constexpr int PER = (UNITS + NT - 1) / NT;
-  const char* base;
-  int64_t ld_bytes;  // bytes between consecutive K
-  int row0, rows, k;
+  static constexpr int kGlobalLoads = PER * VEC, kLdsWrites = PER * VEC;
+  __amdgpu_buffer_rsrc_t rsrc;
+  int ld_bytes, k, valid;  // ld_bytes: bytes between consecutive K
   u32x4 v[PER][VEC];
 
   __device__ void init(const char* b, int64_t /*s_mn*/, int64_t s_k, int r0, int nrows, int kk) {
-    base = b;
-    ld_bytes = s_k * ESZ;
-    row0 = r0;
-    rows = nrows;
+    ld_bytes = (int)(s_k * ESZ);
     k = kk;
+    valid = min(ROWS, nrows - r0);
+    const int64_t span = (int64_t)(kk - 1) * ld_bytes + (int64_t)valid * ESZ;
+    rsrc = make_rsrc(b + (int64_t)r0 * ESZ, (uint32_t)span);
   }
-  __device__ __forceinline__ void load(int kt) {
+  __device__ __forceinline__ void issue(int kt, char*) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int q = threadIdx.x + i * NT;
       const int u = q % UM, g = q / UM;
-      const int mn = row0 + u * VEC;
-      const bool okq = (UNITS % NT == 0 || q < UNITS) && mn < rows;
+      const bool okq = (UNITS % NT == 0 || q < UNITS) && u * VEC < valid;  // valid % VEC == 0 here
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const int kk = kt * DTraits<DT>::BKE + g * VEC + j;
-        const bool ok = okq && kk < k;
-        u32x4 z = {0u, 0u, 0u, 0u};
-        v[i][j] = ok ? *(const u32x4*)(base + (int64_t)kk * ld_bytes + (int64_t)mn * ESZ) : z;
+        const uint32_t off = (okq && kk < k) ? (uint32_t)(kk * ld_bytes + u * VEC * ESZ) : kOutOfRange;
+        v[i][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, 0, 0));
       }
     }
   }
-  __device__ __forceinline__ void store(char* lds) {
+  __device__ __forceinline__ void commit(char* lds) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int q = threadIdx.x + i * NT;
@@ -251,11 +277,13 @@ struct LoaderMN {
 // Consecutive threads walk the operand's smaller stride for coalescing.
 template <int DT, int ROWS, int NT>
 struct LoaderG {
+  static constexpr bool kDirect = false;
   static constexpr int ESZ = DTraits<DT>::ESZ;
   static constexpr int BKE = DTraits<DT>::BKE;
   static constexpr int ELEMS = ROWS * BKE;
   static constexpr int PER = (ELEMS + NT - 1) / NT;
   static constexpr int BATCH = 16;
+  static constexpr int kGlobalLoads = 0, kLdsWrites = 0;  // not scheduled: loads happen in commit()
   const char* base;
   int64_t s_mn, s_k;
   int row0, rows, k, kt_pending;
@@ -272,8 +300,8 @@ struct LoaderG {
     const int64_t amn = smn < 0 ? -smn : smn, ak = sk < 0 ? -sk : sk;
     mn_fast = nrows > 1 && (k == 1 || amn < ak);
   }
-  __device__ __forceinline__ void load(int kt) { kt_pending = kt; }
-  __device__ __forceinline__ void store(char* lds) {
+  __device__ __forceinline__ void issue(int kt, char*) { kt_pending = kt; }
+  __device__ __forceinline__ void commit(char* lds) {
     const int kt = kt_pending;
 #pragma unroll
     for (int i0 = 0; i0 < PER; i0 += BATCH) {
@@ -291,12 +319,13 @@ struct LoaderG {
           kk = e % BKE;
         }
         const int gk = kt * BKE + kk;
-        const bool ok = (ELEMS % NT == 0 || e < ELEMS) && (i0 + j < PER) && row0 + r < rows && gk < k;
+        const bool live = (ELEMS % NT == 0 || e < ELEMS) && (i0 + j < PER);
+        const bool ok = live && row0 + r < rows && gk < k;
         const char* p = base + ((int64_t)(row0 + r) * s_mn + (int64_t)gk * s_k) * ESZ;
         if constexpr (ESZ == 4) val[j] = ok ? *(const uint32_t*)p : 0u;
         else val[j] = ok ? (uint32_t)(*(const uint16_t*)p) : 0u;
         const int bytek = kk * ESZ;
-        off[j] = (ELEMS % NT == 0 || e < ELEMS) && (i0 + j < PER) ? lds_off(r, bytek >> 4) + (bytek & 15) : -1;
+        off[j] = live ? lds_off(r, bytek >> 4) + (bytek & 15) : -1;
       }
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
@@ -322,41 +351,71 @@ struct LoaderSel<MODE_G, DT, ROWS, NT> { using type = LoaderG<DT, ROWS, NT>; };
 // MFMA over one LDS stage.  Lane l of a wave covers M (or N) index l%32 of a
 // 32x32 block and K half h = l/32: it reads logical chunks 4h..4h+3 of its row.
 // Both operands use the same K assignment, so each 32x32 accumulator receives
-// the full 128-byte K slice.
+// the full 128-byte K slice.  The operand fragments are double-buffered in
+// registers: the LDS reads of step s+1 are in flight while the MFMAs of step
+// s issue, so the matrix cores do not wait on LDS latency between steps.
+template <int TM, int TN>
+struct Frags {
+  u32x4 a[TM];
+  u32x4 b[TN];
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void load_frags(Frags<TM, TN>& f, const char* lda, const char* ldb, int wr0, int wc0,
+                                           int lr, int c) {
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) f.a[tm] = *(const u32x4*)(lda + lds_off(wr0 + tm * 32 + lr, c));
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) f.b[tn] = *(const u32x4*)(ldb + lds_off(wc0 + tn * 32 + lr, c));
+}
+
 template <int DT, int TM, int TN>
-__device__ __forceinline__ void mfma_stage(const char* lda, const char* ldb, f32x16 (&acc)[TM][TN],
-                                           int wr0, int wc0, int lane) {
-  const int lr = lane & 31, h = lane >> 5;
+__device__ __forceinline__ void mma_frags(const Frags<TM, TN>& f, f32x16 (&acc)[TM][TN]) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int c = h * 4 + s;
-    u32x4 af[TM], bfr[TN];
+  for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) af[tm] = *(const u32x4*)(lda + lds_off(wr0 + tm * 32 + lr, c));
+    for (int tn = 0; tn < TN; ++tn) {
+      if constexpr (DT == DT_F32) {
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) bfr[tn] = *(const u32x4*)(ldb + lds_off(wc0 + tn * 32 + lr, c));
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        if constexpr (DT == DT_F32) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(af[tm][j]),
-                                                               __uint_as_float(bfr[tn][j]),
-                                                               acc[tm][tn], 0, 0, 0);
-        } else if constexpr (DT == DT_BF16) {
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[tm]),
-                                                                __builtin_bit_cast(bf16x8, bfr[tn]),
-                                                                acc[tm][tn], 0, 0, 0);
-        } else {
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, af[tm]),
-                                                               __builtin_bit_cast(f16x8, bfr[tn]),
-                                                               acc[tm][tn], 0, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(f.a[tm][j]), __uint_as_float(f.b[tn][j]),
+                                                             acc[tm][tn], 0, 0, 0);
+      } else if constexpr (DT == DT_BF16) {
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, f.a[tm]),
+                                                              __builtin_bit_cast(bf16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
+      } else {
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, f.a[tm]),
+                                                             __builtin_bit_cast(f16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
       }
     }
   }
+}
+
+// Instruction-order hints for the scheduler (masks: 0x008 MFMA, 0x100 LDS
+// read, 0x200 LDS write, 0x020 global read).  Each helper lays out one MFMA
+// step: NM MFMAs with the other instructions spread evenly between them, so
+// the single wave per SIMD keeps the matrix pipe fed while memory work issues.
+template <int NM, int NR, int NW, int NG>
+__device__ __forceinline__ void sched_step() {
+  // Each step is its own scheduling region (sched_barrier below), so the LDS
+  // reads placed between its MFMAs can only be the next step's fragments.
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    // Reads go first (one per MFMA) so they have the rest of the step to land.
+    if constexpr (NR > 0) {
+      if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (NW > 0) {
+#pragma unroll
+      for (int j = (i * NW) / NM; j < ((i + 1) * NW) / NM; ++j) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+    if constexpr (NG > 0) {
+#pragma unroll
+      for (int j = (i * NG) / NM; j < ((i + 1) * NG) / NM; ++j) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Output tile of this workgroup: XCD-contiguous, then grouped along M.
@@ -462,8 +521,18 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[
 }
 
 // ---------------------------------------------------------------------------
+// Occupancy the register allocation targets: tiles whose accumulators fill
+// the AGPR file run one wave per SIMD and may use the whole register file.
+template <int DT, int BM, int BN, int WM, int WN>
+struct Occupancy {
+  static constexpr int ACC_REGS = (BM / (WM * 32)) * (BN / (WN * 32)) * 16;
+  static constexpr int WAVES = ACC_REGS >= 128 ? 1 : (ACC_REGS >= 64 ? 2 : 4);
+};
+
 template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
-__global__ __launch_bounds__(WM* WN * 64) void fused_gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(WM* WN * 64)
+__attribute__((amdgpu_waves_per_eu(Occupancy<DT, BM, BN, WM, WN>::WAVES, 8)))
+void fused_gemm_kernel(GemmArgs p) {
   constexpr int NT = WM * WN * 64;
   constexpr int ESZ = DTraits<DT>::ESZ;
   constexpr int TM = BM / (WM * 32);
@@ -493,29 +562,73 @@ __global__ __launch_bounds__(WM* WN * 64) void fused_gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
 
+  // Software pipeline over K stages (4 MFMA steps of 32 bytes of K each):
+  //   step 0..2: LDS reads of step s+1 in flight while step s's MFMAs issue;
+  //   step 2:    registers holding stage kt+1 go to the other LDS buffer and
+  //              the global loads of stage kt+2 are issued;
+  //   step 3:    one barrier, then the next stage's step-0 reads overlap the
+  //              last MFMAs of this stage.
+  // The buffer written in step 2 was last read before the previous stage's
+  // barrier, and the buffer read after this barrier was written before it.
+  const int lr = lane & 31, h = lane >> 5;
   const int nk = (p.k * ESZ + kRowBytes - 1) / kRowBytes;
-  la.load(0);
-  lb.load(0);
-  la.store(smem);
-  lb.store(smem + BM * kRowBytes);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    char* cur = smem + (kt & 1) * STAGE;
-    char* nxt = smem + ((kt + 1) & 1) * STAGE;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      la.load(kt + 1);
-      lb.load(kt + 1);
-    }
-    mfma_stage<DT, TM, TN>(cur, cur + BM * kRowBytes, acc, wr0, wc0, lane);
-    if (more) {
-      la.store(nxt);
-      lb.store(nxt + BM * kRowBytes);
-    }
-    __syncthreads();
-  }
+  using LA = typename LoaderSel<AMODE, DT, BM, NT>::type;
+  using LB = typename LoaderSel<BMODE, DT, BN, NT>::type;
+  constexpr bool ANY_DIRECT = LA::kDirect || LB::kDirect;
+  constexpr int NM = TM * TN * (DT == DT_F32 ? 4 : 1);  // MFMAs per step
+  constexpr int NR = TM + TN;                            // LDS reads per step
+  constexpr int NG_DIRECT = (LA::kDirect ? LA::kGlobalLoads : 0) + (LB::kDirect ? LB::kGlobalLoads : 0);
+  constexpr int NG_REG = (LA::kDirect ? 0 : LA::kGlobalLoads) + (LB::kDirect ? 0 : LB::kGlobalLoads);
+  constexpr int NW = LA::kLdsWrites + LB::kLdsWrites;
 
-  // The last loop iteration ended with a barrier, so all of LDS is free.
+  // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage:
+  //   step 0:   direct loaders start DMA of stage kt+1 into the other buffer;
+  //   step 0-2: the LDS reads of step s+1 are in flight while step s's MFMAs
+  //             issue;
+  //   step 2:   register loaders write stage kt+1 into the other buffer;
+  //   step 3:   wait for the DMA, one barrier, then the next stage's step-0
+  //             reads and the register loaders' global reads of stage kt+2
+  //             overlap this stage's last MFMAs.
+  // The other buffer was last read before the previous stage's barrier.  The
+  // body is branch-free: past the last stage every global read is out of
+  // range (zeros) and the extra LDS writes land in a buffer nothing reads.
+  la.issue(0, smem);
+  lb.issue(0, smem + BM * kRowBytes);
+  la.commit(smem);
+  lb.commit(smem + BM * kRowBytes);
+  if constexpr (!LA::kDirect) la.issue(1, nullptr);
+  if constexpr (!LB::kDirect) lb.issue(1, nullptr);
+  if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  Frags<TM, TN> f0, f1;
+  load_frags(f0, smem, smem + BM * kRowBytes, wr0, wc0, lr, h * 4);
+  for (int kt = 0; kt < nk; ++kt) {
+    char* cur = (kt & 1) ? smem + STAGE : smem;
+    char* nxt = (kt & 1) ? smem : smem + STAGE;
+    if constexpr (LA::kDirect) la.issue(kt + 1, nxt);
+    if constexpr (LB::kDirect) lb.issue(kt + 1, nxt + BM * kRowBytes);
+    load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
+    mma_frags<DT>(f0, acc);
+    sched_step<NM, NR, 0, NG_DIRECT>();
+    load_frags(f0, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 2);
+    mma_frags<DT>(f1, acc);
+    sched_step<NM, NR, 0, 0>();
+    load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 3);
+    if constexpr (!LA::kDirect) la.commit(nxt);
+    if constexpr (!LB::kDirect) lb.commit(nxt + BM * kRowBytes);
+    mma_frags<DT>(f0, acc);
+    sched_step<NM, NR, NW, 0>();
+    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): DMA of stage kt+1 landed
+    __syncthreads();
+    load_frags(f0, nxt, nxt + BM * kRowBytes, wr0, wc0, lr, h * 4);
+    if constexpr (!LA::kDirect) la.issue(kt + 2, nullptr);
+    if constexpr (!LB::kDirect) lb.issue(kt + 2, nullptr);
+    mma_frags<DT>(f1, acc);
+    sched_step<NM, NR, 0, NG_REG>();
+  }
+  __syncthreads();
+
+  // All LDS stage reads are complete (barrier above), so LDS is free.
   static_assert(WM * WN * TN * 32 * 32 * 4 <= 2 * STAGE, "epilogue slices must fit in LDS");
   float* buf = (float*)(smem + wave * (TN * 32 * 32 * 4));
   const int row_base = row0 + wr0, col_base = col0 + wc0;

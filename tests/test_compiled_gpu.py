@@ -97,6 +97,7 @@ def test_compiled_transformer_block_matches_cpu_path(gpu):
 
 def test_autotune_on_gpu_gates_and_picks(gpu):
     model, x = _compiled_mlp(gpu)
+    expected = _cpu_reference(model, x)  # before .to(gpu), which moves the module in place
     xg = x.to(gpu)
     compiled = forgeml_amd.compile(model.to(gpu), (xg,), backend="hip")
     _say("autotune")
@@ -106,7 +107,6 @@ def test_autotune_on_gpu_gates_and_picks(gpu):
         assert not rec["rejected"], rec["rejected"]
         assert rec["winner"] in rec["candidates"]
         assert compiled.kernel_configs[name] in kernels.candidates(torch.float32)
-    expected = _cpu_reference(model, x)
     rtol, atol = tolerance(torch.float32, 2048)
     torch.testing.assert_close(compiled(xg).cpu(), expected, rtol=rtol, atol=atol)
 
