@@ -180,6 +180,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=sorted(EXTRA_GEMMS), default=None,
                     help="run one extra GEMM workload only (for profiling) and print its record")
+    ap.add_argument("--tile", default=None, metavar="BMxBNxWAVES",
+                    help="with --only: force this tile configuration instead of the shape heuristic")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -192,8 +194,19 @@ def main() -> int:
         return 2
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.only:
+        config = None
+        if args.tile:
+            from forgeml_amd import kernels
+
+            bm, bn, waves = (int(v) for v in args.tile.lower().split("x"))
+            matches = [c for c in kernels.candidates(EXTRA_GEMMS[args.only][3])
+                       if (c.block_m, c.block_n, c.num_waves) == (bm, bn, waves)]
+            if not matches:
+                print(f"no built tile {args.tile} for this dtype", file=sys.stderr)
+                return 2
+            config = matches[0]
         print(json.dumps(gemm_workload(args.only, *EXTRA_GEMMS[args.only], steps=args.steps, warmup=args.warmup,
-                                       **EXTRA_KW[args.only])), flush=True)
+                                       config=config, **EXTRA_KW[args.only])), flush=True)
         return 0
     if args.calibrate_copy:
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")

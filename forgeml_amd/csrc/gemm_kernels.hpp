@@ -177,7 +177,7 @@ struct LoaderK {
     const int valid_rows = min(ROWS, nrows - r0);
     const int64_t span = (int64_t)(valid_rows - 1) * ld_bytes + kbytes;
     rsrc = make_rsrc(b + (int64_t)r0 * s_mn * DTraits<DT>::ESZ, (uint32_t)span);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int blk = wave + i * NWAVES;
@@ -190,7 +190,8 @@ struct LoaderK {
   // Stage kt's K offset goes in the scalar offset; lanes past the K tail get
   // an out-of-range vector offset.
   __device__ __forceinline__ void issue(int kt, char* stage) {
-    const int wave = threadIdx.x >> 6;
+    // The wave index is uniform: keep the LDS destination (M0) in SGPRs.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kbase = kt * kRowBytes;
     const int klimit = kbytes - kbase;
 #pragma unroll

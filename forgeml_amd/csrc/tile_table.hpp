@@ -14,4 +14,5 @@
 #define FORGEML_H16_TILES(X) \
   X(256, 256, 2, 2)          \
   X(128, 128, 2, 2)          \
-  X(64, 64, 2, 2)
+  X(64, 64, 2, 2)            \
+  X(256, 256, 2, 4)

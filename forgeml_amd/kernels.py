@@ -51,7 +51,7 @@ DEFAULT_CONFIG = KernelConfig()
 # The library's tile table, in config-id order (forgeml_amd/csrc/tile_table.hpp).
 # A CPU test checks it against forgeml_hip_config_info.
 _FP32_TILES = ((128, 128, 4), (64, 64, 4), (256, 128, 8))
-_H16_TILES = ((256, 256, 4), (128, 128, 4), (64, 64, 4))
+_H16_TILES = ((256, 256, 4), (128, 128, 4), (64, 64, 4), (256, 256, 8))
 CANDIDATES: tuple[KernelConfig, ...] = tuple(
     [KernelConfig(bm, bn, 32, w, 2) for bm, bn, w in _FP32_TILES]
     + [KernelConfig(bm, bn, 64, w, 2) for bm, bn, w in _H16_TILES]
