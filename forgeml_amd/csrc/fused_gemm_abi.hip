@@ -79,24 +79,30 @@ static int combo_of(int ma, int mb) {
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Shape heuristic behind FORGEML_CONFIG_AUTO: the largest tile that still
-// gives every one of the 256 CUs at least one workgroup.
-static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype) {
+// gives every one of the 256 CUs at least one workgroup (the smallest tile
+// otherwise).  Among equal areas, more waves per workgroup win (two waves
+// per SIMD hide each other's stalls), but only where both operands are
+// K-contiguous: the 8-wave tile's register budget does not fit the
+// transposing loaders.
+static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int combo) {
   const int dclass = dclass_of(dtype);
-  int best = -1;
-  int64_t best_area = -1;
-  int smallest = -1;
-  int64_t smallest_area = INT64_MAX;
+  int best = -1, smallest = -1;
+  int64_t best_area = -1, smallest_area = INT64_MAX;
+  int best_waves = 0;
   for (int id = 0; id < kNumTiles; ++id) {
     const TileConfig& t = kTiles[id];
     if (t.dclass != dclass) continue;
+    const int waves = t.wm * t.wn;
+    if (waves > 4 && dclass == 1 && combo != COMBO_K_K) continue;
     const int64_t area = (int64_t)t.bm * t.bn;
     if (area < smallest_area) {
       smallest_area = area;
       smallest = id;
     }
     const int64_t tiles = cdiv(m, t.bm) * cdiv(n, t.bn);
-    if (tiles >= 256 && area > best_area) {
+    if (tiles >= 256 && (area > best_area || (area == best_area && waves > best_waves))) {
       best_area = area;
+      best_waves = waves;
       best = id;
     }
   }
@@ -133,7 +139,7 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype) {
   if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "select_config: M, N, K must be positive");
-  return select_config(m, n, k, dtype);
+  return select_config(m, n, k, dtype, COMBO_K_K);
 }
 
 int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t dtype, int32_t config_id) {
@@ -159,11 +165,8 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   if (act < FORGEML_ACT_NONE || act > FORGEML_ACT_RELU) return set_error(FORGEML_EINVAL, "unknown activation %d", act);
   if (sam < 0 || sak < 0 || sbk < 0 || sbn < 0 || sbi < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
 
-  if (config_id == FORGEML_CONFIG_AUTO) config_id = select_config(m, n, k, dtype);
-  if (config_id < 0 || config_id >= kNumTiles) return set_error(FORGEML_ECONFIG, "config id %d out of range [0, %d)", config_id, kNumTiles);
-  const TileConfig& t = kTiles[config_id];
-  if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
-    return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
+  if (config_id != FORGEML_CONFIG_AUTO && (config_id < 0 || config_id >= kNumTiles))
+    return set_error(FORGEML_ECONFIG, "config id %d out of range [0, %d)", config_id, kNumTiles);
 
   const int esz = esize_of(dtype);
   // A size-1 dimension has no meaningful stride; zero it so layout detection
@@ -176,6 +179,11 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   }
   const int ma = operand_mode(a, m, sam, sak, k, esz);
   const int mb = operand_mode(b, n, sbn, sbk, k, esz);
+  const int combo = combo_of(ma, mb);
+  if (config_id == FORGEML_CONFIG_AUTO) config_id = select_config(m, n, k, dtype, combo);
+  const TileConfig& t = kTiles[config_id];
+  if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
+    return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
 
   GemmArgs p;
   p.a = (const char*)a;
@@ -196,7 +204,7 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.tiles_n = (int)cdiv(n, t.bn);
   p.group_m = p.tiles_m < 8 ? p.tiles_m : 8;
   if ((int64_t)p.tiles_m * p.tiles_n > INT_MAX) return set_error(FORGEML_EINVAL, "too many output tiles");
-  return t.launch[dtype](p, combo_of(ma, mb), (hipStream_t)stream);
+  return t.launch[dtype](p, combo, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -75,23 +75,13 @@ __device__ __forceinline__ int lds_off(int r, int c) {
 }
 
 // ---------------------------------------------------------------------------
-// Element conversions.  bf16 rounding is round-to-nearest-even with NaN kept
-// quiet, the rounding torch's `.to(torch.bfloat16)` performs.
+// Element conversions.
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);
-}
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
 }
 __device__ __forceinline__ float f16_to_f32(uint32_t bits) {
   _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits);
   return (float)h;
-}
-__device__ __forceinline__ uint32_t f32_to_f16(float f) {
-  return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
 template <int DT>
@@ -101,19 +91,34 @@ __device__ __forceinline__ float load_as_f32(const char* p) {
   else return f16_to_f32(*(const uint16_t*)p);
 }
 
-// Round a float to the output dtype and back (identity for fp32).
+// Round a float to the output dtype and back (identity for fp32).  gfx950
+// converts fp32 -> bf16 in hardware (v_cvt_pk_bf16_f32, round to nearest even).
 template <int DT>
 __device__ __forceinline__ float round_to(float v) {
   if constexpr (DT == DT_F32) return v;
-  else if constexpr (DT == DT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else if constexpr (DT == DT_BF16) return (float)(__bf16)v;
   else return (float)(_Float16)v;
 }
 
 template <int DT>
 __device__ __forceinline__ void store_from_f32(char* p, float v) {
   if constexpr (DT == DT_F32) *(float*)p = v;
-  else if constexpr (DT == DT_BF16) *(uint16_t*)p = (uint16_t)f32_to_bf16(v);
-  else *(uint16_t*)p = (uint16_t)f32_to_f16(v);
+  else if constexpr (DT == DT_BF16) *(__bf16*)p = (__bf16)v;
+  else *(_Float16*)p = (_Float16)v;
+}
+
+// Two floats packed into one dword of the 16-bit output dtype.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  if constexpr (DT == DT_BF16) {
+    typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+  }
 }
 
 // GELU from its definition: x/2 (1 + erf(x/sqrt 2)), and the tanh form
@@ -125,11 +130,35 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float inner = 0.79788456080286535588f * (x + 0.044715f * x * x * x);
   return 0.5f * x * (1.0f + tanhf(inner));
 }
-__device__ __forceinline__ float apply_act(float v, int act) {
-  if (act == ACT_GELU_ERF) return gelu_erf(v);
-  if (act == ACT_GELU_TANH) return gelu_tanh(v);
-  if (act == ACT_RELU) return v < 0.0f ? 0.0f : v;  // clamp_min keeps NaN
-  return v;
+
+// Cheaper forms for 16-bit outputs, whose rounding (2^-9 relative for bf16)
+// is far coarser than their error.
+//  * erf GELU = x * Phi(x), with Phi(-|x|) = erfc(|x|/sqrt 2)/2 from
+//    Abramowitz & Stegun 7.1.26: erfc(z) = t(a1 + t(a2 + t(a3 + t(a4 + t a5))))
+//    exp(-z^2), t = 1/(1 + p z), |error| <= 1.5e-7.
+//  * tanh GELU = x * sigmoid(2u) = x / (1 + exp(-2u)), an identity of the
+//    tanh form.
+__device__ __forceinline__ float gelu_erf_16(float x) {
+  const float z = fabsf(x) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float q = 0.5f * poly * t * __expf(-z * z);  // Phi(-|x|)
+  return x * (x >= 0.0f ? 1.0f - q : q);
+}
+__device__ __forceinline__ float gelu_tanh_16(float x) {
+  const float u = 0.79788456080286535588f * fmaf(0.044715f * x, x * x, x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
+}
+
+template <int DT, int ACT>
+__device__ __forceinline__ float activate(float v) {
+  if constexpr (ACT == ACT_GELU_ERF) return DT == DT_F32 ? gelu_erf(v) : gelu_erf_16(v);
+  else if constexpr (ACT == ACT_GELU_TANH) return DT == DT_F32 ? gelu_tanh(v) : gelu_tanh_16(v);
+  else if constexpr (ACT == ACT_RELU) return v < 0.0f ? 0.0f : v;  // clamp_min keeps NaN
+  else return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -448,23 +477,34 @@ __device__ __forceinline__ void wave_sync() {
 //
 // Accumulator element i of a block sits at row 8*(i/4) + 4*(lane/32) + i%4
 // and column lane%32.  Each band of TN blocks (32 rows) is written to the
-// wave's own slice of the (now idle) LDS, then read back so that every lane
-// owns 16 output bytes of one row: the epilogue math runs in a short loop and
-// the stores are 16-byte vectors along rows.  LDS accesses of one wave
-// complete in program order, so the slice needs no barrier.
+// wave's own slice of the (now idle) LDS and read back so that every lane
+// owns EPV consecutive outputs (16 bytes) of one row: the epilogue math is
+// per row segment and the stores are 16-byte vectors.  A lane's columns
+// within a block are the same for every row, so its bias values are loaded
+// once.  LDS accesses of one wave complete in program order; wave_sync keeps
+// the compiler from reordering them.
 //
 // Order of operations follows the reference kernel (src/forgeml/_triton.py:
 // 43-57): round to the output dtype, add the bias in fp32, round again,
 // activate, store.
-template <int DT, int ACT, int TM, int TN>
+template <int DT, int ACT, int TM, int TN, bool INTERIOR>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[TM][TN], float* buf,
                                          int row_base, int col_base, int lane) {
   constexpr int ESZ = DTraits<DT>::ESZ;
-  constexpr int EPV = 16 / ESZ;          // output elements per lane per step
-  constexpr int CPR = 32 / EPV;          // lane-chunks per 32-column block row
-  constexpr int STEPS = TN * 32 * CPR / 64;
+  constexpr int EPV = 16 / ESZ;      // outputs per lane per row segment
+  constexpr int CPR = 32 / EPV;      // lanes per 32-column block row
+  constexpr int SEGS = 32 * CPR / 64;  // row segments per lane per block
   const int lr = lane & 31, h = lane >> 5;
-  const bool vec_ok = (p.n % EPV) == 0 && (((uintptr_t)p.c) & 15) == 0;
+  const int cq = (lane % CPR) * EPV;  // this lane's first column within a block
+  const bool vec_ok = INTERIOR || ((p.n % EPV) == 0 && (((uintptr_t)p.c) & 15) == 0);
+  float bias[TN][EPV];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int j = 0; j < EPV; ++j) {
+      const int col = col_base + tn * 32 + cq + j;
+      bias[tn][j] = (p.has_bias && (INTERIOR || col < p.n)) ? load_as_f32<DT>(p.bias + (int64_t)col * p.sbi * ESZ) : 0.0f;
+    }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
@@ -472,53 +512,57 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[
 #pragma unroll
       for (int i = 0; i < 16; ++i) buf[(tn * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[tm][tn][i];
     wave_sync();
-#pragma unroll 2
-    for (int st = 0; st < STEPS; ++st) {
-      const int q = st * 64 + lane;
-      const int tn = q / (32 * CPR);
-      const int r = (q / CPR) & 31;
-      const int c0 = (q % CPR) * EPV;
-      const int row = row_base + tm * 32 + r;
-      const int col = col_base + tn * 32 + c0;
-      float v[EPV];
 #pragma unroll
-      for (int j = 0; j < EPV; j += 4) {
-        const float4 f = *(const float4*)&buf[(tn * 32 + r) * 32 + c0 + j];
-        v[j] = f.x;
-        v[j + 1] = f.y;
-        v[j + 2] = f.z;
-        v[j + 3] = f.w;
-      }
+    for (int tn = 0; tn < TN; ++tn) {
 #pragma unroll
-      for (int j = 0; j < EPV; ++j) {
-        float x = round_to<DT>(v[j]);
-        if (p.has_bias && col + j < p.n) x = round_to<DT>(x + load_as_f32<DT>(p.bias + (int64_t)(col + j) * p.sbi * ESZ));
-        v[j] = apply_act(x, ACT);
-      }
-      if (row < p.m) {
-        char* dst = p.c + ((int64_t)row * p.n + col) * ESZ;
-        if (vec_ok && col + EPV <= p.n) {
-          u32x4 w;
-          if constexpr (ESZ == 4) {
+      for (int sg = 0; sg < SEGS; ++sg) {
+        const int r = (sg * 64 + lane) / CPR;
+        const int row = row_base + tm * 32 + r;
+        const int col = col_base + tn * 32 + cq;
+        float v[EPV];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = __float_as_uint(v[j]);
-          } else if constexpr (DT == DT_BF16) {
+        for (int j = 0; j < EPV; j += 4) {
+          const float4 f = *(const float4*)&buf[(tn * 32 + r) * 32 + cq + j];
+          v[j] = f.x;
+          v[j + 1] = f.y;
+          v[j + 2] = f.z;
+          v[j + 3] = f.w;
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = f32_to_bf16(v[2 * j]) | (f32_to_bf16(v[2 * j + 1]) << 16);
+        for (int j = 0; j < EPV; ++j) {
+          float x = round_to<DT>(v[j]);
+          if (p.has_bias) x = round_to<DT>(x + bias[tn][j]);
+          v[j] = activate<DT, ACT>(x);
+        }
+        if (INTERIOR || row < p.m) {
+          char* dst = p.c + ((int64_t)row * p.n + col) * ESZ;
+          if (vec_ok && (INTERIOR || col + EPV <= p.n)) {
+            u32x4 w;
+            if constexpr (ESZ == 4) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) w[j] = __float_as_uint(v[j]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) w[j] = pack2<DT>(v[2 * j], v[2 * j + 1]);
+            }
+            *(u32x4*)dst = w;
           } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = f32_to_f16(v[2 * j]) | (f32_to_f16(v[2 * j + 1]) << 16);
+            for (int j = 0; j < EPV; ++j)
+              if (col + j < p.n) store_from_f32<DT>(dst + j * ESZ, v[j]);
           }
-          *(u32x4*)dst = w;
-        } else {
-#pragma unroll
-          for (int j = 0; j < EPV; ++j)
-            if (col + j < p.n) store_from_f32<DT>(dst + j * ESZ, v[j]);
         }
       }
     }
     wave_sync();
   }
+}
+
+template <int DT, int ACT, int TM, int TN>
+__device__ __forceinline__ void epilogue_dispatch(const GemmArgs& p, const f32x16 (&acc)[TM][TN], float* buf,
+                                                  int row_base, int col_base, int lane, bool interior) {
+  if (interior) epilogue<DT, ACT, TM, TN, true>(p, acc, buf, row_base, col_base, lane);
+  else epilogue<DT, ACT, TM, TN, false>(p, acc, buf, row_base, col_base, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -582,21 +626,26 @@ void fused_gemm_kernel(GemmArgs p) {
   constexpr int NG_REG = (LA::kDirect ? 0 : LA::kGlobalLoads) + (LB::kDirect ? 0 : LB::kGlobalLoads);
   constexpr int NW = LA::kLdsWrites + LB::kLdsWrites;
 
-  // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage:
-  //   step 0:   direct loaders start DMA of stage kt+1 into the other buffer;
+  // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage,
+  // two LDS buffers:
   //   step 0-2: the LDS reads of step s+1 are in flight while step s's MFMAs
   //             issue;
   //   step 2:   register loaders write stage kt+1 into the other buffer;
-  //   step 3:   wait for the DMA, one barrier, then the next stage's step-0
-  //             reads and the register loaders' global reads of stage kt+2
-  //             overlap this stage's last MFMAs.
-  // The other buffer was last read before the previous stage's barrier.  The
-  // body is branch-free: past the last stage every global read is out of
-  // range (zeros) and the extra LDS writes land in a buffer nothing reads.
+  //   step 3:   wait until stage kt+1 has landed, one barrier, then the next
+  //             stage's step-0 reads, the DMA of stage kt+2 into the buffer
+  //             just released and the register loaders' global reads of stage
+  //             kt+2 all overlap this stage's last MFMAs.
+  // A buffer is refilled only after the barrier that follows its last read,
+  // and read only after the barrier that follows its fill.  The DMA of a stage
+  // has four MFMA steps to land.  The body is branch-free: past the last stage
+  // every global read is out of range (zeros) and the extra LDS writes land in
+  // a buffer nothing reads.
   la.issue(0, smem);
   lb.issue(0, smem + BM * kRowBytes);
   la.commit(smem);
   lb.commit(smem + BM * kRowBytes);
+  if constexpr (LA::kDirect) la.issue(1, smem + STAGE);
+  if constexpr (LB::kDirect) lb.issue(1, smem + STAGE + BM * kRowBytes);
   if constexpr (!LA::kDirect) la.issue(1, nullptr);
   if constexpr (!LB::kDirect) lb.issue(1, nullptr);
   if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -606,11 +655,9 @@ void fused_gemm_kernel(GemmArgs p) {
   for (int kt = 0; kt < nk; ++kt) {
     char* cur = (kt & 1) ? smem + STAGE : smem;
     char* nxt = (kt & 1) ? smem : smem + STAGE;
-    if constexpr (LA::kDirect) la.issue(kt + 1, nxt);
-    if constexpr (LB::kDirect) lb.issue(kt + 1, nxt + BM * kRowBytes);
     load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
     mma_frags<DT>(f0, acc);
-    sched_step<NM, NR, 0, NG_DIRECT>();
+    sched_step<NM, NR, 0, 0>();
     load_frags(f0, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 2);
     mma_frags<DT>(f1, acc);
     sched_step<NM, NR, 0, 0>();
@@ -619,13 +666,15 @@ void fused_gemm_kernel(GemmArgs p) {
     if constexpr (!LB::kDirect) lb.commit(nxt + BM * kRowBytes);
     mma_frags<DT>(f0, acc);
     sched_step<NM, NR, NW, 0>();
-    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): DMA of stage kt+1 landed
+    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): stage kt+1 landed
     __syncthreads();
     load_frags(f0, nxt, nxt + BM * kRowBytes, wr0, wc0, lr, h * 4);
+    if constexpr (LA::kDirect) la.issue(kt + 2, cur);
+    if constexpr (LB::kDirect) lb.issue(kt + 2, cur + BM * kRowBytes);
     if constexpr (!LA::kDirect) la.issue(kt + 2, nullptr);
     if constexpr (!LB::kDirect) lb.issue(kt + 2, nullptr);
     mma_frags<DT>(f1, acc);
-    sched_step<NM, NR, 0, NG_REG>();
+    sched_step<NM, NR, 0, NG_DIRECT + NG_REG>();
   }
   __syncthreads();
 
@@ -633,11 +682,14 @@ void fused_gemm_kernel(GemmArgs p) {
   static_assert(WM * WN * TN * 32 * 32 * 4 <= 2 * STAGE, "epilogue slices must fit in LDS");
   float* buf = (float*)(smem + wave * (TN * 32 * 32 * 4));
   const int row_base = row0 + wr0, col_base = col0 + wc0;
+  // Interior tiles (the workgroup's whole tile inside C) skip per-element bounds checks.
+  const bool interior = row0 + BM <= p.m && col0 + BN <= p.n && (p.n % DTraits<DT>::VEC) == 0 &&
+                        (((uintptr_t)p.c) & 15) == 0;
   switch (p.act) {
-    case ACT_GELU_ERF: epilogue<DT, ACT_GELU_ERF, TM, TN>(p, acc, buf, row_base, col_base, lane); break;
-    case ACT_GELU_TANH: epilogue<DT, ACT_GELU_TANH, TM, TN>(p, acc, buf, row_base, col_base, lane); break;
-    case ACT_RELU: epilogue<DT, ACT_RELU, TM, TN>(p, acc, buf, row_base, col_base, lane); break;
-    default: epilogue<DT, ACT_NONE, TM, TN>(p, acc, buf, row_base, col_base, lane); break;
+    case ACT_GELU_ERF: epilogue_dispatch<DT, ACT_GELU_ERF, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
+    case ACT_GELU_TANH: epilogue_dispatch<DT, ACT_GELU_TANH, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
+    case ACT_RELU: epilogue_dispatch<DT, ACT_RELU, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
+    default: epilogue_dispatch<DT, ACT_NONE, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
   }
 }
 

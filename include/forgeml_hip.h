@@ -95,7 +95,8 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
 int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k,
                                         int32_t dtype, int32_t config_id);
 
-/* The config id FORGEML_CONFIG_AUTO resolves to for this shape.
+/* The config id FORGEML_CONFIG_AUTO resolves to for this shape when both
+ * operands are K-contiguous (forgeml_hip_gemm also weighs the layout).
  * Counterpart of DEFAULT_CONFIG (src/forgeml/kernels.py:21). */
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype);
 
