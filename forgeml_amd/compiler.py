@@ -101,12 +101,33 @@ class CompiledModel:
             if alloc is not None:
                 n = alloc.size_bytes // node.spec.dtype.itemsize
                 self._views[node.name] = self._slots[alloc.slot][:n].view(node.spec.shape)
+        self._kernel_layout_constants()
         self._steps = [(node, self._make_step(node)) for node in self.graph.nodes]
+
+    def _kernel_layout_constants(self) -> None:
+        """Store GEMM weights of hip-planned nodes K-contiguous.
+
+        A ``[K, N]`` weight constant becomes the same logical tensor with
+        strides ``(1, K)`` (the ``nn.Linear`` layout), which the gfx950 kernels
+        stream by DMA straight into LDS; the row-major copy would need the
+        transposing register loader.  Values, shape, dtype and device are
+        unchanged, so torch ops on the constant are unaffected.
+        """
+        consts = self.graph.constants
+        for node in self.graph.nodes:
+            if self.kernel_plan.get(node.name) != "hip" or node.op not in kernels.GEMM_OPS:
+                continue
+            name = node.inputs[1]
+            w = consts.get(name)
+            if w is None or w.dim() != 2 or not w.is_contiguous() or w.shape[0] == 1 or w.shape[1] == 1:
+                continue
+            consts[name] = w.t().contiguous().t()
 
     def __setattr__(self, name, value):
         object.__setattr__(self, name, value)
         # A new kernel plan changes dispatch, so rebuild the step closures.
         if name == "kernel_plan" and "_views" in self.__dict__:
+            self._kernel_layout_constants()
             object.__setattr__(self, "_steps", [(n, self._make_step(n)) for n in self.graph.nodes])
 
     def _make_step(self, node):
