@@ -6,6 +6,7 @@
 // bypassed it.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdint>
@@ -60,32 +61,56 @@ static constexpr int64_t kMaxBufferBytes = (int64_t)1 << 31;
 
 static int operand_mode(const void* base, int64_t rows, int64_t s_mn, int64_t s_k, int64_t k, int esz) {
   const int vec = 16 / esz;
-  const bool aligned = ((uintptr_t)base % 16) == 0;
-  if (aligned && s_k == 1 && s_mn >= 0 && (s_mn * esz) % 16 == 0 && k % vec == 0 &&
-      (kMaxPanelRows * s_mn + k) * esz < kMaxBufferBytes)
-    return MODE_K;
-  if (aligned && s_mn == 1 && s_k >= 0 && (s_k * esz) % 16 == 0 && rows % vec == 0 &&
-      (k * s_k + kMaxPanelRows) * esz < kMaxBufferBytes)
-    return MODE_MN;
+  const uintptr_t addr = (uintptr_t)base;
+  // Room for the pipeline's reads one or two stages past K (out of range).
+  const bool k_fits = s_k == 1 && s_mn >= 0 && s_mn < kMaxBufferBytes &&
+                      (kMaxPanelRows * s_mn + k) * esz + 2 * kRowBytes < kMaxBufferBytes;
+  const bool mn_fits = s_mn == 1 && s_k >= 0 && s_k < kMaxBufferBytes && (k * s_k + kMaxPanelRows) * esz < kMaxBufferBytes;
+  if (addr % 16 == 0 && k_fits && (s_mn * esz) % 16 == 0 && k % vec == 0) return MODE_K;
+  if (addr % 16 == 0 && mn_fits && (s_k * esz) % 16 == 0 && rows % vec == 0) return MODE_MN;
+  if (addr % 4 == 0 && k_fits && (s_mn * esz) % 4 == 0 && (k * esz) % 4 == 0) return MODE_K4;
   return MODE_G;
 }
 
-static int combo_of(int ma, int mb) {
-  if (ma == MODE_G || mb == MODE_G) return COMBO_G_G;
-  if (ma == MODE_K) return mb == MODE_K ? COMBO_K_K : COMBO_K_MN;
-  return mb == MODE_K ? COMBO_MN_K : COMBO_MN_MN;
+// The built combination for an operand pair.  A 16-byte K-contiguous operand
+// also meets the 4-byte mode's conditions and any operand can be read by
+// element loads, so pairs without a kernel of their own step down to one that
+// has.  `small_tile` says whether the tile (<= 128x128) has the extra combos.
+static int combo_of(int ma, int mb, bool small_tile) {
+  const bool a_k = ma == MODE_K, b_k = mb == MODE_K;
+  const bool a_kk = a_k || ma == MODE_K4, b_kk = b_k || mb == MODE_K4;
+  if (a_k && b_k) return COMBO_K_K;
+  if (a_k && mb == MODE_MN) return COMBO_K_MN;
+  if (ma == MODE_MN && b_k) return COMBO_MN_K;
+  if (ma == MODE_MN && mb == MODE_MN) return COMBO_MN_MN;
+  if (small_tile) {
+    if (a_kk && b_kk) return COMBO_K4_K4;
+    if (ma == MODE_K4 && mb == MODE_MN) return COMBO_K4_MN;
+    if (mb == MODE_MN) return COMBO_G_MN;
+  }
+  return COMBO_G_G;
+}
+
+static bool needs_small_tile(int ma, int mb) {
+  return combo_of(ma, mb, true) != combo_of(ma, mb, false);
 }
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Shape heuristic behind FORGEML_CONFIG_AUTO: the largest tile that still
 // gives every one of the 256 CUs at least one workgroup (the smallest tile
-// otherwise).  Among equal areas, more waves per workgroup win (two waves
-// per SIMD hide each other's stalls), but only where both operands are
-// K-contiguous: the 8-wave tile's register budget does not fit the
-// transposing loaders.
-static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int combo) {
+// otherwise; split K then adds workgroups).  Among equal areas, more waves
+// per workgroup win (two waves per SIMD hide each other's stalls), but only
+// where both operands are K-contiguous: the 8-wave tile's register budget
+// does not fit the transposing loaders.  Layouts whose kernels exist only for
+// small tiles choose among those, and 16-bit element loads (whose staged
+// values and addresses outgrow the registers of larger tiles) use 64x64.
+static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int ma, int mb) {
   const int dclass = dclass_of(dtype);
+  const bool all_k = ma == MODE_K && mb == MODE_K;
+  const int64_t max_area = (dclass == 1 && (ma == MODE_G || mb == MODE_G)) ? 64 * 64
+                           : needs_small_tile(ma, mb)                     ? kSmallTileArea
+                                                                          : INT64_MAX;
   int best = -1, smallest = -1;
   int64_t best_area = -1, smallest_area = INT64_MAX;
   int best_waves = 0;
@@ -93,8 +118,9 @@ static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int com
     const TileConfig& t = kTiles[id];
     if (t.dclass != dclass) continue;
     const int waves = t.wm * t.wn;
-    if (waves > 4 && dclass == 1 && combo != COMBO_K_K) continue;
+    if (waves > 4 && dclass == 1 && !all_k) continue;
     const int64_t area = (int64_t)t.bm * t.bn;
+    if (area > max_area) continue;
     if (area < smallest_area) {
       smallest_area = area;
       smallest = id;
@@ -107,6 +133,37 @@ static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int com
     }
   }
   return best >= 0 ? best : smallest;
+}
+
+// K split for a grid of few output tiles: enough workgroups for two per CU,
+// slices of at least kMinSliceStages stages, at most kMaxSplit slices.
+static constexpr int64_t kSplitBelowTiles = 128;
+static constexpr int64_t kSplitTargetWgs = 512;
+static constexpr int64_t kMinSliceStages = 4;
+static constexpr int64_t kMaxSplit = 16;
+
+struct SplitPlan {
+  int splits;  // 1 = no split
+  int kslice;  // stages per slice
+};
+
+static SplitPlan split_plan(const TileConfig& t, int64_t m, int64_t n, int64_t k, int esz) {
+  const int64_t tiles = cdiv(m, t.bm) * cdiv(n, t.bn);
+  const int64_t nk = cdiv(k * esz, kRowBytes);
+  SplitPlan plan{1, (int)nk};
+  if (tiles >= kSplitBelowTiles) return plan;
+  int64_t s = cdiv(kSplitTargetWgs, tiles);
+  s = std::min(s, nk / kMinSliceStages);
+  s = std::min(s, kMaxSplit);
+  if (s < 2) return plan;
+  const int64_t slice = cdiv(nk, s);
+  plan.kslice = (int)slice;
+  plan.splits = (int)cdiv(nk, slice);  // every slice non-empty
+  return plan;
+}
+
+static int64_t workspace_bytes_for(const SplitPlan& plan, int64_t m, int64_t n) {
+  return plan.splits > 1 ? (int64_t)plan.splits * m * n * (int64_t)sizeof(float) : 0;
 }
 
 }  // namespace forgeml
@@ -131,7 +188,7 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
   out[3] = t.dclass == 0 ? kRowBytes / 4 : kRowBytes / 2;
   out[4] = t.wm * t.wn;
   out[5] = 2;
-  out[6] = 1;
+  out[6] = (int32_t)kMaxSplit;
   out[7] = 2 * (t.bm + t.bn) * kRowBytes;
   return FORGEML_OK;
 }
@@ -139,7 +196,7 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype) {
   if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "select_config: M, N, K must be positive");
-  return select_config(m, n, k, dtype, COMBO_K_K);
+  return select_config(m, n, k, dtype, MODE_K, MODE_K);
 }
 
 int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t dtype, int32_t config_id) {
@@ -147,14 +204,23 @@ int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "workspace_size: M, N, K must be positive");
   if (config_id != FORGEML_CONFIG_AUTO && (config_id < 0 || config_id >= kNumTiles))
     return set_error(FORGEML_ECONFIG, "config id %d out of range", config_id);
-  return 0;
+  if (config_id != FORGEML_CONFIG_AUTO && kTiles[config_id].dclass != dclass_of(dtype))
+    return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
+  const int esz = esize_of(dtype);
+  if (config_id != FORGEML_CONFIG_AUTO) return workspace_bytes_for(split_plan(kTiles[config_id], m, n, k, esz), m, n);
+  // The automatic tile depends on the operands' layout: cover every choice.
+  static const int kModePairs[][2] = {{MODE_K, MODE_K}, {MODE_K, MODE_MN}, {MODE_K4, MODE_K4}, {MODE_G, MODE_MN}};
+  int64_t most = 0;
+  for (const auto& mp : kModePairs) {
+    const int id = select_config(m, n, k, dtype, mp[0], mp[1]);
+    most = std::max(most, workspace_bytes_for(split_plan(kTiles[id], m, n, k, esz), m, n));
+  }
+  return most;
 }
 
 int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
                      const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
                      int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   g_last_error[0] = '\0';
   if (a == nullptr || b == nullptr || c == nullptr) return set_error(FORGEML_EINVAL, "a, b and c must be non-NULL");
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "M, N, K must be positive (got %lld, %lld, %lld)",
@@ -179,11 +245,19 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   }
   const int ma = operand_mode(a, m, sam, sak, k, esz);
   const int mb = operand_mode(b, n, sbn, sbk, k, esz);
-  const int combo = combo_of(ma, mb);
-  if (config_id == FORGEML_CONFIG_AUTO) config_id = select_config(m, n, k, dtype, combo);
+  if (config_id == FORGEML_CONFIG_AUTO) config_id = select_config(m, n, k, dtype, ma, mb);
   const TileConfig& t = kTiles[config_id];
   if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
     return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
+  const int combo = combo_of(ma, mb, (int64_t)t.bm * t.bn <= kSmallTileArea);
+  const SplitPlan plan = split_plan(t, m, n, k, esz);
+  const int64_t ws_need = workspace_bytes_for(plan, m, n);
+  if (ws_need > 0) {
+    if (workspace == nullptr || workspace_bytes < ws_need)
+      return set_error(FORGEML_EWORKSPACE, "this shape splits K %d ways and needs %lld workspace bytes (got %lld)",
+                       plan.splits, (long long)ws_need, (long long)(workspace == nullptr ? 0 : workspace_bytes));
+    if (((uintptr_t)workspace & 15) != 0) return set_error(FORGEML_EWORKSPACE, "workspace must be 16-byte aligned");
+  }
 
   GemmArgs p;
   p.a = (const char*)a;
@@ -203,7 +277,10 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.tiles_m = (int)cdiv(m, t.bm);
   p.tiles_n = (int)cdiv(n, t.bn);
   p.group_m = p.tiles_m < 8 ? p.tiles_m : 8;
-  if ((int64_t)p.tiles_m * p.tiles_n > INT_MAX) return set_error(FORGEML_EINVAL, "too many output tiles");
+  p.splits = plan.splits;
+  p.kslice = plan.kslice;
+  p.ws = ws_need > 0 ? (float*)workspace : nullptr;
+  if ((int64_t)p.tiles_m * p.tiles_n * plan.splits > INT_MAX) return set_error(FORGEML_EINVAL, "too many output tiles");
   return t.launch[dtype](p, combo, (hipStream_t)stream);
 }
 

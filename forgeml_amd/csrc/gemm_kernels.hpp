@@ -42,7 +42,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
-enum : int { MODE_K = 0, MODE_MN = 1, MODE_G = 2 };
+enum : int { MODE_K = 0, MODE_MN = 1, MODE_G = 2, MODE_K4 = 3 };
 enum : int { ACT_NONE = 0, ACT_GELU_ERF = 1, ACT_GELU_TANH = 2, ACT_RELU = 3 };
 
 constexpr int kRowBytes = 128;  // bytes of K per LDS row and per stage
@@ -60,6 +60,12 @@ struct GemmArgs {
   int has_bias;
   int tiles_m, tiles_n;
   int group_m;
+  // Split K: `splits` workgroups share each output tile, slice z covering
+  // stages [z*kslice, (z+1)*kslice).  With splits > 1 each slice stores its
+  // raw fp32 sums to ws[z][M][N] and splitk_reduce_kernel applies the
+  // epilogue.  splits == 1: kslice is the whole K, ws is unused.
+  int splits, kslice;
+  float* ws;
 };
 
 template <int DT>
@@ -200,7 +206,7 @@ struct LoaderK {
   uint32_t voff[PER];  // this lane's byte offset in stage 0, or out of range
   int kchunk[PER];     // byte offset of this lane's chunk within a stage
 
-  __device__ void init(const char* b, int64_t s_mn, int64_t /*s_k*/, int r0, int nrows, int k) {
+  __device__ __forceinline__ void init(const char* b, int64_t s_mn, int64_t /*s_k*/, int r0, int nrows, int k) {
     const int ld_bytes = (int)(s_mn * DTraits<DT>::ESZ);
     kbytes = k * DTraits<DT>::ESZ;
     const int valid_rows = min(ROWS, nrows - r0);
@@ -235,6 +241,59 @@ struct LoaderK {
   __device__ __forceinline__ void commit(char*) {}
 };
 
+// K contiguous with rows only 4-byte aligned (e.g. an odd fp32 K): DMA one
+// dword per lane.  A wave's buffer_load_dword ... lds writes 256 contiguous
+// LDS bytes = 2 rows; lane L lands at byte 4*L, i.e. row L/32, physical chunk
+// (L%32)/4, dword L%4, and fetches the dword of the logical chunk stored
+// there.  For row pair `blk` (rows 2blk, 2blk+1) the swizzle term
+// (r ^ r>>3) & 7 is (2blk ^ blk>>2 ^ L/32) & 7, so a lane's chunk is its own
+// constant XOR a wave-uniform value, and the row pair's base offset goes in
+// the scalar offset with the stage's K offset.
+template <int DT, int ROWS, int NT>
+struct LoaderK4 {
+  static constexpr bool kDirect = true;
+  static constexpr int BLOCKS = ROWS / 2;
+  static constexpr int NWAVES = NT / 64;
+  static constexpr int PER = (BLOCKS + NWAVES - 1) / NWAVES;
+  static constexpr int kGlobalLoads = PER, kLdsWrites = 0;
+  __amdgpu_buffer_rsrc_t rsrc;
+  int kbytes, ld_bytes, valid_rows;
+  int lane_off;  // (L/32)*ld_bytes + (L%4)*4
+  int lane_c;    // ((L%32)/4 ^ L/32) & 7
+  int lane_dw;   // (L%4)*4
+  int lane_r;    // L/32
+
+  __device__ __forceinline__ void init(const char* b, int64_t s_mn, int64_t /*s_k*/, int r0, int nrows, int k) {
+    ld_bytes = (int)(s_mn * DTraits<DT>::ESZ);
+    kbytes = k * DTraits<DT>::ESZ;
+    valid_rows = min(ROWS, nrows - r0);
+    const int64_t span = (int64_t)(valid_rows - 1) * ld_bytes + kbytes;
+    rsrc = make_rsrc(b + (int64_t)r0 * s_mn * DTraits<DT>::ESZ, (uint32_t)span);
+    const int lane = threadIdx.x & 63;
+    lane_r = lane >> 5;
+    lane_dw = (lane & 3) * 4;
+    lane_off = lane_r * ld_bytes + lane_dw;
+    lane_c = (((lane & 31) >> 2) ^ lane_r) & 7;
+  }
+  __device__ __forceinline__ void issue(int kt, char* stage) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kbase = kt * kRowBytes;
+    const int klimit = kbytes - kbase;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int blk = wave + i * NWAVES;  // uniform per wave
+      if (BLOCKS % NWAVES == 0 || blk < BLOCKS) {
+        const int cb = ((lane_c ^ (2 * blk) ^ (blk >> 2)) & 7) * 16;
+        const bool ok = 2 * blk + lane_r < valid_rows && cb + lane_dw < klimit;
+        const uint32_t off = ok ? (uint32_t)(lane_off + cb) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(stage + blk * 256), 4, off,
+                                                 kbase + 2 * blk * ld_bytes, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void commit(char*) {}
+};
+
 // M/N contiguous: each unit is VEC rows x VEC K values, fetched as VEC
 // 16-byte vectors along M/N (one per K value) into registers and transposed
 // there into one 16-byte LDS chunk per row.
@@ -251,7 +310,7 @@ struct LoaderMN {
   int ld_bytes, k, valid;  // ld_bytes: bytes between consecutive K
   u32x4 v[PER][VEC];
 
-  __device__ void init(const char* b, int64_t /*s_mn*/, int64_t s_k, int r0, int nrows, int kk) {
+  __device__ __forceinline__ void init(const char* b, int64_t /*s_mn*/, int64_t s_k, int r0, int nrows, int kk) {
     ld_bytes = (int)(s_k * ESZ);
     k = kk;
     valid = min(ROWS, nrows - r0);
@@ -303,66 +362,98 @@ struct LoaderMN {
   }
 };
 
-// Any strides: element loads, issued when the stage is written to LDS.
-// Consecutive threads walk the operand's smaller stride for coalescing.
+// Any strides: element loads.  Consecutive threads walk the operand's
+// smaller stride for coalescing; either way a thread's elements of a stage lie
+// on one line of the stage, (r0 + i*dr, kk0 + i*dk), because the thread count
+// is a multiple of both ROWS and the stage's K extent.  Up to 32 elements per
+// thread are held in registers from issue() to commit(), so the loads overlap
+// the MFMAs like the vector loaders'; larger tiles load in commit().
 template <int DT, int ROWS, int NT>
 struct LoaderG {
   static constexpr bool kDirect = false;
   static constexpr int ESZ = DTraits<DT>::ESZ;
   static constexpr int BKE = DTraits<DT>::BKE;
   static constexpr int ELEMS = ROWS * BKE;
-  static constexpr int PER = (ELEMS + NT - 1) / NT;
+  static constexpr int PER = ELEMS / NT;
+  static constexpr bool kStaged = PER <= 16;
   static constexpr int BATCH = 16;
-  static constexpr int kGlobalLoads = 0, kLdsWrites = 0;  // not scheduled: loads happen in commit()
-  const char* base;
-  int64_t s_mn, s_k;
-  int row0, rows, k, kt_pending;
-  bool mn_fast;
+  static constexpr int kGlobalLoads = kStaged ? PER : 0, kLdsWrites = kStaged ? PER : 0;
+  static_assert(ELEMS % NT == 0 && NT % ROWS == 0 && NT % BKE == 0, "thread count must tile the stage");
+  const char* safe;      // element (row0, 0): always inside the operand
+  const char* p0;        // this thread's first element of stage 0
+  int64_t step_bytes;    // between a thread's consecutive elements of a stage
+  int64_t stage_bytes;   // between stages (BKE * s_k elements)
+  int r0, kk0, dr, dk, rows_left, k;
+  int kt_pending;
+  // Staged values; 16-bit elements are packed two to a register.
+  static constexpr int NVAL = kStaged ? (ESZ == 4 ? PER : (PER + 1) / 2) : 1;
+  uint32_t val[NVAL];
 
-  __device__ void init(const char* b, int64_t smn, int64_t sk, int r0, int nrows, int kk) {
-    base = b;
-    s_mn = smn;
-    s_k = sk;
-    row0 = r0;
-    rows = nrows;
+  __device__ __forceinline__ void init(const char* b, int64_t smn, int64_t sk, int row0, int nrows, int kk) {
+    const int64_t amn = smn < 0 ? -smn : smn, ak = sk < 0 ? -sk : sk;
+    const bool mn_fast = nrows > 1 && (kk == 1 || amn < ak);
+    const int t = threadIdx.x;
+    if (mn_fast) {
+      r0 = t % ROWS;
+      kk0 = t / ROWS;
+      dr = 0;
+      dk = NT / ROWS;
+    } else {
+      r0 = t / BKE;
+      kk0 = t % BKE;
+      dr = NT / BKE;
+      dk = 0;
+    }
+    safe = b + (int64_t)row0 * smn * ESZ;
+    p0 = b + ((int64_t)(row0 + r0) * smn + (int64_t)kk0 * sk) * ESZ;
+    step_bytes = ((int64_t)dr * smn + (int64_t)dk * sk) * ESZ;
+    stage_bytes = (int64_t)BKE * sk * ESZ;
+    rows_left = nrows - row0;
     k = kk;
     kt_pending = 0;
-    const int64_t amn = smn < 0 ? -smn : smn, ak = sk < 0 ? -sk : sk;
-    mn_fast = nrows > 1 && (k == 1 || amn < ak);
   }
-  __device__ __forceinline__ void issue(int kt, char*) { kt_pending = kt; }
-  __device__ __forceinline__ void commit(char* lds) {
-    const int kt = kt_pending;
+  // Branch-free: a lane outside the operand reads the always-valid element
+  // and discards it.
+  __device__ __forceinline__ uint32_t fetch(int i, int kt) const {
+    const bool ok = r0 + i * dr < rows_left && kt * BKE + kk0 + i * dk < k;
+    const char* p = ok ? p0 + kt * stage_bytes + i * step_bytes : safe;
+    uint32_t v;
+    if constexpr (ESZ == 4) v = *(const uint32_t*)p;
+    else v = *(const uint16_t*)p;
+    return ok ? v : 0u;
+  }
+  __device__ __forceinline__ void put(char* lds, int i, uint32_t v) const {
+    const int bytek = (kk0 + i * dk) * ESZ;
+    char* dst = lds + lds_off(r0 + i * dr, bytek >> 4) + (bytek & 15);
+    if constexpr (ESZ == 4) *(uint32_t*)dst = v;
+    else *(uint16_t*)dst = (uint16_t)v;
+  }
+  __device__ __forceinline__ void issue(int kt, char*) {
+    if constexpr (kStaged) {
+      if constexpr (ESZ == 4) {
 #pragma unroll
-    for (int i0 = 0; i0 < PER; i0 += BATCH) {
-      uint32_t val[BATCH];
-      int off[BATCH];
+        for (int i = 0; i < PER; ++i) val[i] = fetch(i, kt);
+      } else {
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const int e = threadIdx.x + (i0 + j) * NT;
-        int r, kk;
-        if (mn_fast) {
-          r = e % ROWS;
-          kk = e / ROWS;
-        } else {
-          r = e / BKE;
-          kk = e % BKE;
-        }
-        const int gk = kt * BKE + kk;
-        const bool live = (ELEMS % NT == 0 || e < ELEMS) && (i0 + j < PER);
-        const bool ok = live && row0 + r < rows && gk < k;
-        const char* p = base + ((int64_t)(row0 + r) * s_mn + (int64_t)gk * s_k) * ESZ;
-        if constexpr (ESZ == 4) val[j] = ok ? *(const uint32_t*)p : 0u;
-        else val[j] = ok ? (uint32_t)(*(const uint16_t*)p) : 0u;
-        const int bytek = kk * ESZ;
-        off[j] = live ? lds_off(r, bytek >> 4) + (bytek & 15) : -1;
+        for (int i = 0; i < PER; i += 2)
+          val[i / 2] = fetch(i, kt) | (i + 1 < PER ? fetch(i + 1, kt) << 16 : 0u);
       }
+    } else {
+      kt_pending = kt;
+    }
+  }
+  __device__ __forceinline__ void commit(char* lds) {
+    if constexpr (kStaged) {
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        if (off[j] >= 0) {
-          if constexpr (ESZ == 4) *(uint32_t*)(lds + off[j]) = val[j];
-          else *(uint16_t*)(lds + off[j]) = (uint16_t)val[j];
-        }
+      for (int i = 0; i < PER; ++i) put(lds, i, ESZ == 4 ? val[i] : (val[i / 2] >> (16 * (i & 1))) & 0xffffu);
+    } else {
+#pragma unroll
+      for (int i0 = 0; i0 < PER; i0 += BATCH) {
+        uint32_t v[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) v[j] = fetch(i0 + j, kt_pending);
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) put(lds, i0 + j, v[j]);
       }
     }
   }
@@ -376,6 +467,8 @@ template <int DT, int ROWS, int NT>
 struct LoaderSel<MODE_MN, DT, ROWS, NT> { using type = LoaderMN<DT, ROWS, NT>; };
 template <int DT, int ROWS, int NT>
 struct LoaderSel<MODE_G, DT, ROWS, NT> { using type = LoaderG<DT, ROWS, NT>; };
+template <int DT, int ROWS, int NT>
+struct LoaderSel<MODE_K4, DT, ROWS, NT> { using type = LoaderK4<DT, ROWS, NT>; };
 
 // ---------------------------------------------------------------------------
 // MFMA over one LDS stage.  Lane l of a wave covers M (or N) index l%32 of a
@@ -448,13 +541,16 @@ __device__ __forceinline__ void sched_step() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Output tile of this workgroup: XCD-contiguous, then grouped along M.
-__device__ __forceinline__ void tile_coords(const GemmArgs& p, int& pm, int& pn) {
-  const int nwg = p.tiles_m * p.tiles_n;
+// Output tile and K slice of this workgroup: XCD-contiguous, the K slices of
+// a tile adjacent, tiles grouped along M.
+__device__ __forceinline__ void tile_coords(const GemmArgs& p, int& pm, int& pn, int& z) {
+  const int nwg = p.tiles_m * p.tiles_n * p.splits;
   const int b = blockIdx.x;
   const int xcd = b & 7, local = b >> 3;
   const int full = nwg >> 3, rem = nwg & 7;
-  const int lin = xcd * full + (xcd < rem ? xcd : rem) + local;
+  const int lin_all = xcd * full + (xcd < rem ? xcd : rem) + local;
+  const int lin = lin_all / p.splits;
+  z = lin_all - lin * p.splits;
   const int per_group = p.group_m * p.tiles_n;
   const int g = lin / per_group;
   const int first_m = g * p.group_m;
@@ -568,15 +664,20 @@ __device__ __forceinline__ void epilogue_dispatch(const GemmArgs& p, const f32x1
 // ---------------------------------------------------------------------------
 // Occupancy the register allocation targets: tiles whose accumulators fill
 // the AGPR file run one wave per SIMD and may use the whole register file.
-template <int DT, int BM, int BN, int WM, int WN>
+// 16-bit tiles whose loaders stage through registers (M/N-contiguous or
+// element loads) hold 8 vectors or 32 packed elements per operand in flight,
+// so they are given the register budget of two waves per SIMD.
+template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
 struct Occupancy {
   static constexpr int ACC_REGS = (BM / (WM * 32)) * (BN / (WN * 32)) * 16;
-  static constexpr int WAVES = ACC_REGS >= 128 ? 1 : (ACC_REGS >= 64 ? 2 : 4);
+  static constexpr bool REG_STAGED = DT != DT_F32 && (AMODE == MODE_MN || AMODE == MODE_G || BMODE == MODE_MN ||
+                                                      BMODE == MODE_G);
+  static constexpr int WAVES = ACC_REGS >= 128 ? 1 : ((ACC_REGS >= 64 || REG_STAGED) ? 2 : 4);
 };
 
 template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
 __global__ __launch_bounds__(WM* WN * 64)
-__attribute__((amdgpu_waves_per_eu(Occupancy<DT, BM, BN, WM, WN>::WAVES, 8)))
+__attribute__((amdgpu_waves_per_eu(Occupancy<DT, BM, BN, WM, WN, AMODE, BMODE>::WAVES, 8)))
 void fused_gemm_kernel(GemmArgs p) {
   constexpr int NT = WM * WN * 64;
   constexpr int ESZ = DTraits<DT>::ESZ;
@@ -586,14 +687,19 @@ void fused_gemm_kernel(GemmArgs p) {
   static_assert(TM * WM * 32 == BM && TN * WN * 32 == BN, "tile must split into 32x32 blocks");
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
-  int pm, pn;
-  tile_coords(p, pm, pn);
+  int pm, pn, z;
+  tile_coords(p, pm, pn, z);
   const int row0 = pm * BM, col0 = pn * BN;
+  // This workgroup's K stages [kt0, kt0 + nks); the loaders treat the slice
+  // end as the end of K, so nothing past it is read.
+  const int kt0 = z * p.kslice;
+  const int nks = min((p.k * ESZ + kRowBytes - 1) / kRowBytes - kt0, p.kslice);
+  const int kend = min(p.k, (kt0 + nks) * DTraits<DT>::BKE);
 
   typename LoaderSel<AMODE, DT, BM, NT>::type la;
   typename LoaderSel<BMODE, DT, BN, NT>::type lb;
-  la.init(p.a, p.sam, p.sak, row0, p.m, p.k);
-  lb.init(p.b, p.sbn, p.sbk, col0, p.n, p.k);
+  la.init(p.a, p.sam, p.sak, row0, p.m, kend);
+  lb.init(p.b, p.sbn, p.sbk, col0, p.n, kend);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wr0 = (wave / WN) * (TM * 32);
@@ -616,7 +722,6 @@ void fused_gemm_kernel(GemmArgs p) {
   // The buffer written in step 2 was last read before the previous stage's
   // barrier, and the buffer read after this barrier was written before it.
   const int lr = lane & 31, h = lane >> 5;
-  const int nk = (p.k * ESZ + kRowBytes - 1) / kRowBytes;
   using LA = typename LoaderSel<AMODE, DT, BM, NT>::type;
   using LB = typename LoaderSel<BMODE, DT, BN, NT>::type;
   constexpr bool ANY_DIRECT = LA::kDirect || LB::kDirect;
@@ -640,21 +745,22 @@ void fused_gemm_kernel(GemmArgs p) {
   // has four MFMA steps to land.  The body is branch-free: past the last stage
   // every global read is out of range (zeros) and the extra LDS writes land in
   // a buffer nothing reads.
-  la.issue(0, smem);
-  lb.issue(0, smem + BM * kRowBytes);
+  la.issue(kt0, smem);
+  lb.issue(kt0, smem + BM * kRowBytes);
   la.commit(smem);
   lb.commit(smem + BM * kRowBytes);
-  if constexpr (LA::kDirect) la.issue(1, smem + STAGE);
-  if constexpr (LB::kDirect) lb.issue(1, smem + STAGE + BM * kRowBytes);
-  if constexpr (!LA::kDirect) la.issue(1, nullptr);
-  if constexpr (!LB::kDirect) lb.issue(1, nullptr);
+  if constexpr (LA::kDirect) la.issue(kt0 + 1, smem + STAGE);
+  if constexpr (LB::kDirect) lb.issue(kt0 + 1, smem + STAGE + BM * kRowBytes);
+  if constexpr (!LA::kDirect) la.issue(kt0 + 1, nullptr);
+  if constexpr (!LB::kDirect) lb.issue(kt0 + 1, nullptr);
   if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   Frags<TM, TN> f0, f1;
   load_frags(f0, smem, smem + BM * kRowBytes, wr0, wc0, lr, h * 4);
-  for (int kt = 0; kt < nk; ++kt) {
-    char* cur = (kt & 1) ? smem + STAGE : smem;
-    char* nxt = (kt & 1) ? smem : smem + STAGE;
+  for (int it = 0; it < nks; ++it) {
+    const int kt = kt0 + it;
+    char* cur = (it & 1) ? smem + STAGE : smem;
+    char* nxt = (it & 1) ? smem : smem + STAGE;
     load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
     mma_frags<DT>(f0, acc);
     sched_step<NM, NR, 0, 0>();
@@ -682,6 +788,15 @@ void fused_gemm_kernel(GemmArgs p) {
   static_assert(WM * WN * TN * 32 * 32 * 4 <= 2 * STAGE, "epilogue slices must fit in LDS");
   float* buf = (float*)(smem + wave * (TN * 32 * 32 * 4));
   const int row_base = row0 + wr0, col_base = col0 + wc0;
+  if (p.splits > 1) {
+    // K slice: raw fp32 sums to this slice's plane of the workspace.
+    GemmArgs q = p;
+    q.c = (char*)(p.ws + (int64_t)z * p.m * p.n);
+    q.has_bias = 0;
+    const bool interior_ws = row0 + BM <= p.m && col0 + BN <= p.n && (p.n % 4) == 0 && (((uintptr_t)q.c) & 15) == 0;
+    epilogue_dispatch<DT_F32, ACT_NONE, TM, TN>(q, acc, buf, row_base, col_base, lane, interior_ws);
+    return;
+  }
   // Interior tiles (the workgroup's whole tile inside C) skip per-element bounds checks.
   const bool interior = row0 + BM <= p.m && col0 + BN <= p.n && (p.n % DTraits<DT>::VEC) == 0 &&
                         (((uintptr_t)p.c) & 15) == 0;
@@ -690,6 +805,62 @@ void fused_gemm_kernel(GemmArgs p) {
     case ACT_GELU_TANH: epilogue_dispatch<DT, ACT_GELU_TANH, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
     case ACT_RELU: epilogue_dispatch<DT, ACT_RELU, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
     default: epilogue_dispatch<DT, ACT_NONE, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K epilogue: C = act(rnd(rnd(sum_z ws[z]) + bias)), the slices summed
+// in order z = 0, 1, ... so results do not depend on scheduling.  Each thread
+// owns 4 consecutive elements of C (row-major, flattened).
+struct ReduceArgs {
+  const float* ws;
+  const char* bias;
+  char* c;
+  int64_t sbi;
+  int64_t mn;  // M * N
+  int n, splits, has_bias;
+  int vec;     // mn % 4 == 0 and ws, c aligned for 4-element vectors
+};
+
+template <int DT, int ACT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs p) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e0 >= p.mn) return;
+  const int cnt = p.mn - e0 < 4 ? (int)(p.mn - e0) : 4;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (p.vec) {
+    for (int z = 0; z < p.splits; ++z) {
+      const float4 w = *(const float4*)(p.ws + (int64_t)z * p.mn + e0);
+      v[0] += w.x;
+      v[1] += w.y;
+      v[2] += w.z;
+      v[3] += w.w;
+    }
+  } else {
+    for (int z = 0; z < p.splits; ++z)
+      for (int j = 0; j < cnt; ++j) v[j] += p.ws[(int64_t)z * p.mn + e0 + j];
+  }
+  int col = (int)(e0 % p.n);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float x = round_to<DT>(v[j]);
+    if (p.has_bias && j < cnt) x = round_to<DT>(x + load_as_f32<DT>(p.bias + (int64_t)col * p.sbi * ESZ));
+    v[j] = activate<DT, ACT>(x);
+    col = col + 1 == p.n ? 0 : col + 1;
+  }
+  char* dst = p.c + e0 * ESZ;
+  if (p.vec) {
+    if constexpr (ESZ == 4) {
+      *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint2 w;
+      w.x = pack2<DT>(v[0], v[1]);
+      w.y = pack2<DT>(v[2], v[3]);
+      *(uint2*)dst = w;
+    }
+  } else {
+    for (int j = 0; j < cnt; ++j) store_from_f32<DT>(dst + j * ESZ, v[j]);
   }
 }
 

@@ -16,13 +16,44 @@ enum : int {
   COMBO_MN_K = 2,
   COMBO_MN_MN = 3,
   COMBO_G_G = 4,   // any strides
-  NUM_COMBOS = 5,
+  // Built for tiles of at most 128x128 (kSmallTileArea); larger tiles use G_G.
+  COMBO_K4_K4 = 5,  // both K-contiguous with rows only 4-byte aligned (odd fp32 K)
+  COMBO_K4_MN = 6,  // A as above, B N-contiguous
+  COMBO_G_MN = 7,   // A any strides (e.g. an odd 16-bit K), B N-contiguous
+  NUM_COMBOS = 8,
 };
+
+constexpr int kSmallTileArea = 128 * 128;
 
 // Sets the thread-local error text; returns `code`.
 int set_error(int code, const char* fmt, ...);
 
 constexpr int kMaxDevices = 64;
+
+// The split-K epilogue kernel over the workspace planes of one GEMM.
+template <int DT>
+int launch_reduce(const GemmArgs& p, hipStream_t stream) {
+  ReduceArgs r;
+  r.ws = p.ws;
+  r.bias = p.bias;
+  r.c = p.c;
+  r.sbi = p.sbi;
+  r.mn = (int64_t)p.m * p.n;
+  r.n = p.n;
+  r.splits = p.splits;
+  r.has_bias = p.has_bias;
+  r.vec = r.mn % 4 == 0 && ((uintptr_t)p.ws & 15) == 0 && ((uintptr_t)p.c & 15) == 0;
+  const dim3 grid((unsigned)((r.mn + 1023) / 1024)), block(256);
+  switch (p.act) {
+    case ACT_GELU_ERF: hipLaunchKernelGGL((splitk_reduce_kernel<DT, ACT_GELU_ERF>), grid, block, 0, stream, r); break;
+    case ACT_GELU_TANH: hipLaunchKernelGGL((splitk_reduce_kernel<DT, ACT_GELU_TANH>), grid, block, 0, stream, r); break;
+    case ACT_RELU: hipLaunchKernelGGL((splitk_reduce_kernel<DT, ACT_RELU>), grid, block, 0, stream, r); break;
+    default: hipLaunchKernelGGL((splitk_reduce_kernel<DT, ACT_NONE>), grid, block, 0, stream, r); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(-3, "split-K reduce launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
 
 template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
 int launch_one(const GemmArgs& p, hipStream_t stream) {
@@ -44,14 +75,22 @@ int launch_one(const GemmArgs& p, hipStream_t stream) {
     }
   }
   hipLaunchKernelGGL((fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE>),
-                     dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(NT), LDS, stream, p);
+                     dim3((unsigned)(p.tiles_m * p.tiles_n * p.splits)), dim3(NT), LDS, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(-3, "kernel launch failed: %s", hipGetErrorString(e));
-  return 0;
+  return p.splits > 1 ? launch_reduce<DT>(p, stream) : 0;
 }
 
 template <int DT, int BM, int BN, int WM, int WN>
 int launch_tile(const GemmArgs& p, int combo, hipStream_t stream) {
+  if constexpr (BM * BN <= kSmallTileArea) {
+    switch (combo) {
+      case COMBO_K4_K4: return launch_one<DT, BM, BN, WM, WN, MODE_K4, MODE_K4>(p, stream);
+      case COMBO_K4_MN: return launch_one<DT, BM, BN, WM, WN, MODE_K4, MODE_MN>(p, stream);
+      case COMBO_G_MN: return launch_one<DT, BM, BN, WM, WN, MODE_G, MODE_MN>(p, stream);
+      default: break;
+    }
+  }
   switch (combo) {
     case COMBO_K_K: return launch_one<DT, BM, BN, WM, WN, MODE_K, MODE_K>(p, stream);
     case COMBO_K_MN: return launch_one<DT, BM, BN, WM, WN, MODE_K, MODE_MN>(p, stream);

@@ -180,6 +180,62 @@ def test_every_config_and_layout(gpu, dtype):
             _gate(got, expected, k, what)
 
 
+# -- rows not 16-byte aligned, and split K ----------------------------------------
+#
+# Odd K (fp32 rows 4-byte aligned: dword DMA; 16-bit rows 2-byte aligned:
+# element loads) and K = 2 mod 8 (16-bit rows 4-byte aligned: dword DMA),
+# with B as W^T or as contiguous [K,N].  The small grids (a few 64x64 or
+# 128x128 tiles) split K over workgroups and reduce through the workspace.
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+@pytest.mark.parametrize("m,n,k", [(392, 328, 521), (392, 328, 522), (1000, 1024, 522), (3, 200, 2049)])
+def test_unaligned_k_layouts(gpu, dtype, m, n, k):
+    seed = case_seed("unaligned", m, n, k, dtype)
+    a, b_nt, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout="nt")
+    expected = reference_cpu(a, b_nt, bias, "gelu")
+    a_d, bias_d = a.to(gpu), bias.to(gpu)
+    layouts = {"nt": to_gpu(b_nt, gpu), "nn": b_nt.contiguous().to(gpu)}
+    for config in (kernels.DEFAULT_CONFIG,) + kernels.candidates(dtype):
+        for name, b_d in layouts.items():
+            what = f"M={m} N={n} K={k} {dtype} B={name} config={config} seed={seed}"
+            _say(what)
+            got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=config)
+            _gate(got, expected, k, what)
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_split_k_epilogues(gpu, dtype):
+    m, n, k = 5, 640, 3000
+    seed = case_seed("split_k", dtype)
+    a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+    ws = kernels.workspace_for(m, n, k, dtype, -1, gpu)
+    assert ws is not None, "this skinny shape is expected to split K"
+    a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+    for with_bias in (False, True):
+        for activation, approximate in (("none", "none"), ("gelu", "none"), ("gelu", "tanh"), ("relu", "none")):
+            what = f"split-K {dtype} bias={with_bias} act={activation}/{approximate} seed={seed}"
+            _say(what)
+            got = kernels.matmul(a_d, b_d, bias_d if with_bias else None, activation=activation,
+                                 approximate=approximate)
+            _gate(got, reference_cpu(a, b, bias if with_bias else None, activation, approximate), k, what)
+    # The slices are summed in a fixed order: repeated calls are bit-identical.
+    first = kernels.matmul(a_d, b_d, bias_d, activation="gelu")
+    assert torch.equal(first, kernels.matmul(a_d, b_d, bias_d, activation="gelu"))
+
+
+def test_split_k_workspace_is_checked(gpu):
+    m, n, k = 1, 768, 4096
+    a, b, _ = gemm_inputs(m, n, k, torch.float32, seed=case_seed("ws_check"), bias=False)
+    a_d, b_d = a.to(gpu), to_gpu(b, gpu)
+    out = torch.empty(m, n, device=gpu)
+    _say("split-K workspace check")
+    with pytest.raises(RuntimeError, match="workspace"):
+        kernels.launch(a_d, b_d, None, out, act=0, config_id=-1, workspace=None)
+    ws = kernels.workspace_for(m, n, k, torch.float32, -1, gpu)
+    kernels.launch(a_d, b_d, None, out, act=0, config_id=-1, workspace=ws)
+    _gate(out, reference_cpu(a, b), k, "split-K explicit workspace")
+
+
 def test_deterministic(gpu):
     a, b, bias = gemm_inputs(512, 768, 1024, torch.bfloat16, seed=case_seed("det"))
     a, b, bias = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)

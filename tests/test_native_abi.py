@@ -36,7 +36,7 @@ def test_config_table_matches_python_candidates():
     for info, cfg in zip(table, kernels.CANDIDATES):
         dclass, bm, bn, bk, waves, stages, split, lds = info
         assert (bm, bn, bk, waves, stages) == (cfg.block_m, cfg.block_n, cfg.block_k, cfg.num_waves, cfg.num_stages)
-        assert dclass == (0 if cfg.block_k == 32 else 1) and split == 1
+        assert dclass == (0 if cfg.block_k == 32 else 1) and split == 16
         assert lds == 2 * (bm + bn) * 128 and lds <= 160 * 1024
 
 
@@ -76,3 +76,41 @@ def test_matmul_boundary_validation_on_cpu():
         kernels._check_config(kernels.candidates(torch.bfloat16)[0], torch.float32)
     assert kernels._check_config(kernels.DEFAULT_CONFIG, torch.float32) == _native.CONFIG_AUTO
     assert "fused_gemm_kernel" in kernels.kernel_source() and "__global__" in kernels.kernel_source()
+
+
+def test_split_k_workspace_size():
+    lib = _native.load()
+    f32 = _native.DTYPE_F32
+    # Few output tiles and a long K: the K reduction is split over workgroups
+    # and each slice needs an fp32 M x N plane.
+    for m, n, k in [(1, 768, 4096), (33, 3072, 1531), (7, 768, 768)]:
+        for dtype in (f32, _native.DTYPE_BF16):
+            ws = lib.forgeml_hip_gemm_workspace_size(m, n, k, dtype, -1)
+            plane = m * n * 4
+            assert ws > 0 and ws % plane == 0 and 2 <= ws // plane <= 16, (m, n, k, dtype, ws)
+    # Enough tiles to fill the GPU, or too little K to split: no workspace.
+    assert lib.forgeml_hip_gemm_workspace_size(4096, 4096, 4096, f32, -1) == 0
+    assert lib.forgeml_hip_gemm_workspace_size(1, 768, 64, f32, -1) == 0
+    # An explicit small tile on a small grid splits too; the largest tile on a
+    # grid that fills the GPU does not.
+    small = next(i for i, info in enumerate(_native.config_table()) if info[0] == 0 and info[1] == 64)
+    assert lib.forgeml_hip_gemm_workspace_size(64, 64, 8192, f32, small) > 0
+    assert lib.forgeml_hip_gemm_workspace_size(8192, 8192, 8192, f32, small) == 0
+    # A 16-bit config id for an fp32 problem is rejected.
+    h16 = next(i for i, info in enumerate(_native.config_table()) if info[0] == 1)
+    assert lib.forgeml_hip_gemm_workspace_size(64, 64, 8192, f32, h16) == _native.ECONFIG
+
+
+def test_split_k_needs_workspace():
+    lib = _native.load()
+    dummy = ctypes.c_void_p(16)  # never dereferenced: the workspace check fails before any launch
+    m, n, k = 1, 768, 4096
+    need = lib.forgeml_hip_gemm_workspace_size(m, n, k, _native.DTYPE_F32, -1)
+    assert need > 0
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, None, 0, None)
+    assert rc == _native.EWORKSPACE and "workspace" in _native.last_error()
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, dummy, need - 4, None)
+    assert rc == _native.EWORKSPACE
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, ctypes.c_void_p(20), need,
+                              None)
+    assert rc == _native.EWORKSPACE and "aligned" in _native.last_error()
