@@ -101,21 +101,110 @@ def gemm_workload(name, m, n, k, dtype, *, steps, warmup, act="gelu", bias=True,
     }
 
 
-def compiled_workload(name, model, x, *, steps, warmup):
-    """CompiledModel forward latency on the GPU (hip backend), host wall clock."""
+def _graph_per_call_us(calls, replays: int = 10) -> float:
+    """Capture `calls` (a list of launch closures) into one HIP graph and return the
+    mean GPU time per captured call over `replays` replays (HIP events)."""
+    for fn in calls[:3]:
+        fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in calls[:2]:
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in calls:
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (replays * len(calls))
+
+
+SKINNY_POOL_BYTES = 320 << 20  # weights rotate through more than the 256 MB Infinity Cache
+
+
+def skinny_workload(m, n, k, dtype):
+    """HBM-bound skinny GEMM (C = GELU(A W^T + bias), M tiny): GPU time per call inside a
+    HIP graph, the weight read from a rotating pool larger than the Infinity Cache."""
+    from forgeml_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    esz = torch.tensor([], dtype=dtype).element_size()
+    nbuf = max(2, -(-SKINNY_POOL_BYTES // (n * k * esz)))
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = (torch.randn(m, k, generator=g, device=dev) * k ** -0.25).to(dtype)
+    weights = [(torch.randn(n, k, generator=g, device=dev) * k ** -0.25).to(dtype) for _ in range(nbuf)]
+    bias = (torch.rand(n, generator=g, device=dev) * 0.2 - 0.1).to(dtype)
+    out = torch.empty(m, n, dtype=dtype, device=dev)
+    ws = kernels.workspace_for(m, n, k, dtype, -1, dev)
+    act = kernels._act_code("gelu", "none")
+    calls = [lambda w=w: kernels.launch(a, w.t(), bias, out, act=act, config_id=-1, workspace=ws) for w in weights]
+    us = _graph_per_call_us(calls)
+    algo_bytes = (m * k + k * n + m * n + n) * esz
+    resolved = kernels.resolve_config(m, n, k, dtype)
+    del weights
+    return {
+        "workload": f"skinny_{DTYPE_NAMES[dtype]}_{m}x{n}x{k}_bias_gelu",
+        "shape": [m, n, k],
+        "dtype": DTYPE_NAMES[dtype],
+        "us_per_call_in_graph": round(us, 2),
+        "algorithmic_bytes": algo_bytes,
+        "GB_per_s": round(algo_bytes / us / 1e3, 1),
+        "hbm_frac": round(algo_bytes / us / 1e3 / HBM_GBPS, 4),
+        "tile": [resolved.block_m, resolved.block_n],
+        "split_k_planes": 0 if ws is None else ws.numel() // (m * n * 4),
+    }
+
+
+SKINNY_SHAPES = [(m, n, k, dt) for dt in (torch.float32, torch.bfloat16) for m in (1, 33)
+                 for n, k in ((3072, 1024), (3000, 1531))]
+
+
+def compiled_workload(name, make_model, make_input, *, steps, warmup, cpu_budget_s=20.0):
+    """CompiledModel forward latency (synchronized host wall clock, as the reference
+    times it): eager hip backend, the same captured in a HIP graph, and the
+    reference's CPU path (the model compiled with the torch backend, on the host)."""
     import forgeml_amd
     from forgeml_amd.measurement import measure_variants
 
     dev = torch.device("cuda", 0)
-    model = model.to(dev).eval()
-    x = x.to(dev)
+    model_cpu, x_cpu = make_model(), make_input()
+    compiled_cpu = forgeml_amd.compile(model_cpu, (x_cpu,), backend="torch")
+    cpu = []
+    t_end = time.perf_counter() + cpu_budget_s
+    with torch.inference_mode():
+        compiled_cpu(x_cpu)
+        while len(cpu) < 10 and (len(cpu) < 3 or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            compiled_cpu(x_cpu)
+            cpu.append((time.perf_counter() - t0) * 1e3)
+    model = make_model().to(dev).eval()
+    x = x_cpu.to(dev)
     compiled = forgeml_amd.compile(model, (x,), backend="hip")
-    timings = measure_variants({"hip": lambda: compiled(x)}, device=dev, warmup=warmup, repeats=max(steps, 2))
+    graphed = compiled.capture_graph(x)
+    timings = measure_variants({"hip": lambda: compiled(x), "hip_graph": lambda: graphed(x)}, device=dev,
+                               warmup=warmup, repeats=max(steps, 2))
+    cpu_ms = statistics.median(cpu)
     return {
         "workload": name,
         "kernel_plan": sorted(set(compiled.kernel_plan.values())),
-        "median_us": timings["hip"]["median_ms"] * 1e3,
-        "p95_us": timings["hip"]["p95_ms"] * 1e3,
+        "hip_median_us": round(timings["hip"]["median_ms"] * 1e3, 1),
+        "hip_p95_us": round(timings["hip"]["p95_ms"] * 1e3, 1),
+        "hip_graph_median_us": round(timings["hip_graph"]["median_ms"] * 1e3, 1),
+        "hip_graph_p95_us": round(timings["hip_graph"]["p95_ms"] * 1e3, 1),
+        "cpu_reference_median_us": round(cpu_ms * 1e3, 1),
+        "cpu_reference_threads": torch.get_num_threads(),
+        "cpu_reference_samples": len(cpu),
+        "speedup_vs_cpu_graph": round(cpu_ms * 1e3 / (timings["hip_graph"]["median_ms"] * 1e3), 1),
     }
 
 
@@ -251,15 +340,26 @@ def main() -> int:
                  for name in EXTRA_GEMMS]
         from forgeml_amd.neural import TransformerBlock, make_mlp
 
-        torch.manual_seed(0)
-        mlp = make_mlp(512, 2048, 512)
-        torch.manual_seed(1)
-        extra.append(compiled_workload("compiled_mlp_64x512x2048_fp32", mlp, torch.randn(64, 512),
-                                       steps=25, warmup=5))
-        torch.manual_seed(0)
-        block = TransformerBlock(768, 12, 3072).eval()
-        extra.append(compiled_workload("compiled_transformer_block_8x512x768_fp32", block,
-                                       torch.randn(8, 512, 768), steps=10, warmup=3))
+        def mlp():
+            torch.manual_seed(0)
+            return make_mlp(512, 2048, 512).eval()
+
+        def mlp_input():
+            torch.manual_seed(1)
+            return torch.randn(64, 512)
+
+        def block():
+            torch.manual_seed(0)
+            return TransformerBlock(768, 12, 3072).eval()
+
+        def block_input():
+            torch.manual_seed(1)
+            return torch.randn(8, 512, 768)
+
+        extra.append(compiled_workload("compiled_mlp_64x512x2048_fp32", mlp, mlp_input, steps=50, warmup=5))
+        extra.append(compiled_workload("compiled_transformer_block_8x512x768_fp32", block, block_input,
+                                       steps=10, warmup=3))
+        result["skinny"] = [skinny_workload(*shape) for shape in SKINNY_SHAPES]
         result["extra"] = extra
     print(json.dumps(result), flush=True)
     return 0

@@ -6,7 +6,7 @@ for gfx950 (CDNA4 MFMA) and called through a C ABI (include/forgeml_hip.h).
 """
 
 from forgeml_amd.analysis import graph_analysis
-from forgeml_amd.compiler import CompiledModel, compile
+from forgeml_amd.compiler import CompiledModel, GraphedModel, compile
 from forgeml_amd.frontend import from_torch
 from forgeml_amd.ir import Graph, GraphBuilder, GraphError, TensorSpec
 from forgeml_amd.neural import TransformerBlock
@@ -15,6 +15,7 @@ __all__ = [
     "CompiledModel",
     "Graph",
     "GraphBuilder",
+    "GraphedModel",
     "GraphError",
     "TensorSpec",
     "TransformerBlock",

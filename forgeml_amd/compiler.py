@@ -217,6 +217,10 @@ class CompiledModel:
             )
         raise GraphError(f"no hip kernel for op {node.op!r}")
 
+    def capture_graph(self, *example_inputs: torch.Tensor, warmup: int = 2) -> "GraphedModel":
+        """Capture one call into a HIP graph for these input shapes (see GraphedModel)."""
+        return GraphedModel(self, example_inputs, warmup=warmup)
+
     def explain(self) -> dict:
         analysis = graph_analysis(self.graph)
         original = graph_analysis(self.original_graph)
@@ -241,6 +245,57 @@ class CompiledModel:
                 "planned_bytes": self.memory_plan.naive_bytes - self.memory_plan.planned_bytes,
             },
         }
+
+
+class GraphedModel:
+    """A CompiledModel call captured once into a HIP graph and replayed.
+
+    The per-node host work of ``CompiledModel.__call__`` (closures, kernel
+    argument validation, launches; src/forgeml/compiler.py:158-164) is paid
+    once at capture; a call then copies the inputs into the graph's static
+    input buffers and replays every kernel of the model as one graph launch.
+    The slot arena, the weights and the graph's own memory pool stay
+    resident.  Outputs are the graph's static output tensors: the next call
+    overwrites them, so clone what must be kept.  Like the compiled model, a
+    graphed model is not reentrant.
+
+    Shapes, dtypes and devices are fixed by the example inputs.  Capture runs
+    ``warmup`` eager calls first, on a side stream, so the kernels' one-time
+    set-up (library load, LDS limits) happens outside the graph.
+    """
+
+    def __init__(self, compiled: CompiledModel, example_inputs, *, warmup: int = 2):
+        inputs = compiled._check_inputs(tuple(example_inputs))
+        devices = {t.device for t in inputs.values()}
+        if len(devices) != 1 or next(iter(devices)).type != "cuda":
+            raise GraphError("graph capture needs every input on one GPU")
+        self.compiled = compiled
+        self.device = next(iter(devices))
+        self._static_inputs = [t.clone() for t in inputs.values()]
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(max(1, warmup)):
+                compiled(*self._static_inputs)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.device(self.device), torch.cuda.graph(self.graph):
+            self._static_output = compiled(*self._static_inputs)
+        torch.cuda.synchronize(self.device)
+
+    def __call__(self, *inputs: torch.Tensor):
+        values = self.compiled._check_inputs(inputs)
+        for dst, src in zip(self._static_inputs, values.values()):
+            if src.data_ptr() != dst.data_ptr():
+                dst.copy_(src)
+        self.graph.replay()
+        return self._static_output
+
+    @property
+    def static_inputs(self) -> list[torch.Tensor]:
+        """The graph's input buffers: writing them directly skips the copy."""
+        return self._static_inputs
 
 
 def compile(

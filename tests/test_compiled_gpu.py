@@ -128,3 +128,50 @@ def test_mixed_plan_relu_residual(gpu):
     assert "hip" in c.kernel_plan.values() and "torch" in c.kernel_plan.values()
     _say("mixed plan")
     torch.testing.assert_close(c(x.to(gpu)).cpu(), expected, rtol=1e-4, atol=1e-4)
+
+
+# -- HIP-graph capture of a compiled model --------------------------------------
+
+def _graph_replays_match_eager(compiled, make_input, rtol=0.0, atol=0.0, replays=3):
+    graphed = compiled.capture_graph(make_input(0))
+    for r in range(1, replays + 1):
+        x = make_input(r)
+        _say("graph replay", r)
+        got = graphed(x).clone()
+        # Eager work of the program between replays, on the same arena.
+        eager = compiled(x)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, eager, rtol=rtol, atol=atol)
+    return graphed
+
+
+def test_graphed_mlp_matches_eager_and_cpu(gpu):
+    model, x = _compiled_mlp(gpu)
+    expected = _cpu_reference(model, x)
+    compiled = forgeml_amd.compile(model.to(gpu), (x.to(gpu),), backend="hip")
+
+    def make_input(r):
+        g = torch.Generator().manual_seed(100 + r)
+        return torch.randn(64, 512, generator=g).to(gpu)
+
+    graphed = _graph_replays_match_eager(compiled, make_input)
+    rtol, atol = tolerance(torch.float32, 2048)
+    torch.testing.assert_close(graphed(x.to(gpu)).cpu(), expected, rtol=rtol, atol=atol)
+
+
+def test_graphed_transformer_block_matches_eager(gpu):
+    torch.manual_seed(0)
+    block = TransformerBlock(768, 12, 3072).eval()
+    torch.manual_seed(1)
+    x = torch.randn(8, 512, 768)
+    expected = _cpu_reference(block, x)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    compiled = forgeml_amd.compile(block.to(gpu), (x.to(gpu),), backend="hip")
+
+    def make_input(r):
+        g = torch.Generator().manual_seed(200 + r)
+        return torch.randn(8, 512, 768, generator=g).to(gpu)
+
+    graphed = _graph_replays_match_eager(compiled, make_input, rtol=1e-6, atol=1e-6)
+    rtol, atol = tolerance(torch.float32, 3072)
+    torch.testing.assert_close(graphed(x.to(gpu)).cpu(), expected, rtol=rtol * 10, atol=atol * 10)

@@ -130,6 +130,29 @@ def test_gpu_dispatch_path_with_fake_kernel(monkeypatch):
     assert seen == [("gelu", "tanh", True, True), ("none", "none", True, False)]
 
 
+def test_hip_plan_stores_weights_k_contiguous(monkeypatch):
+    monkeypatch.setattr(kernels, "matmul", _fake_matmul([]))
+    model = make_mlp()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(model, (x,))
+    before = {k: v.clone() for k, v in c.graph.constants.items()}
+    c.kernel_plan = {n.name: "hip" for n in c.graph.nodes}
+    for node in c.graph.nodes:
+        w = c.graph.constants[node.inputs[1]]
+        k, n = w.shape
+        # Same logical [K, N] values, stored as nn.Linear stores its weight.
+        assert w.stride() == (1, k) and torch.equal(w, before[node.inputs[1]])
+    torch.testing.assert_close(c(x), model(x))
+
+
+def test_graph_capture_requires_gpu_inputs():
+    model = make_mlp()
+    x = torch.randn(4, 8)
+    c = forgeml_amd.compile(model, (x,))
+    with pytest.raises(GraphError, match="one GPU"):
+        c.capture_graph(x)
+
+
 def test_hip_plan_on_view_op_is_rejected():
     b = GraphBuilder({"x": spec(2, 4)})
     b.add("r", "reshape", ("x",), shape=(8,))
