@@ -145,12 +145,13 @@ def skinny_workload(m, n, k, dtype):
     weights = [(torch.randn(n, k, generator=g, device=dev) * k ** -0.25).to(dtype) for _ in range(nbuf)]
     bias = (torch.rand(n, generator=g, device=dev) * 0.2 - 0.1).to(dtype)
     out = torch.empty(m, n, dtype=dtype, device=dev)
-    ws = kernels.workspace_for(m, n, k, dtype, -1, dev)
+    plan = kernels.plan(a, weights[0].t())
+    ws = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev) if plan["workspace_bytes"] else None
     act = kernels._act_code("gelu", "none")
     calls = [lambda w=w: kernels.launch(a, w.t(), bias, out, act=act, config_id=-1, workspace=ws) for w in weights]
     us = _graph_per_call_us(calls)
     algo_bytes = (m * k + k * n + m * n + n) * esz
-    resolved = kernels.resolve_config(m, n, k, dtype)
+    cfg = plan["config"]
     del weights
     return {
         "workload": f"skinny_{DTYPE_NAMES[dtype]}_{m}x{n}x{k}_bias_gelu",
@@ -160,8 +161,9 @@ def skinny_workload(m, n, k, dtype):
         "algorithmic_bytes": algo_bytes,
         "GB_per_s": round(algo_bytes / us / 1e3, 1),
         "hbm_frac": round(algo_bytes / us / 1e3 / HBM_GBPS, 4),
-        "tile": [resolved.block_m, resolved.block_n],
-        "split_k_planes": 0 if ws is None else ws.numel() // (m * n * 4),
+        "kernel": plan["kernel"],
+        "tile": [cfg.block_m, cfg.block_n],
+        "k_splits": plan["k_splits"],
     }
 
 

@@ -25,6 +25,9 @@ namespace forgeml {
   extern template int launch_tile<DT_F16, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
 FORGEML_F32_TILES(FORGEML_EXTERN_F32)
 FORGEML_H16_TILES(FORGEML_EXTERN_H16)
+extern template int launch_skinny<DT_F32>(const GemmArgs&, int, hipStream_t);
+extern template int launch_skinny<DT_BF16>(const GemmArgs&, int, hipStream_t);
+extern template int launch_skinny<DT_F16>(const GemmArgs&, int, hipStream_t);
 #undef FORGEML_EXTERN_F32
 #undef FORGEML_EXTERN_H16
 
@@ -40,12 +43,15 @@ int set_error(int code, const char* fmt, ...) {
 
 static const TileConfig kTiles[] = {
 #define FORGEML_ROW_F32(bm, bn, wm, wn) \
-  {0, bm, bn, wm, wn, {&launch_tile<DT_F32, bm, bn, wm, wn>, nullptr, nullptr}},
+  {0, bm, bn, wm, wn, KIND_TILED, {&launch_tile<DT_F32, bm, bn, wm, wn>, nullptr, nullptr}},
 #define FORGEML_ROW_H16(bm, bn, wm, wn) \
-  {1, bm, bn, wm, wn, {nullptr, &launch_tile<DT_BF16, bm, bn, wm, wn>, &launch_tile<DT_F16, bm, bn, wm, wn>}},
+  {1, bm, bn, wm, wn, KIND_TILED, {nullptr, &launch_tile<DT_BF16, bm, bn, wm, wn>, &launch_tile<DT_F16, bm, bn, wm, wn>}},
     FORGEML_F32_TILES(FORGEML_ROW_F32) FORGEML_H16_TILES(FORGEML_ROW_H16)
 #undef FORGEML_ROW_F32
 #undef FORGEML_ROW_H16
+    // Few-row kernels (M <= 64, K-contiguous operands), last so the tiled ids stay put.
+    {0, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {&launch_skinny<DT_F32>, nullptr, nullptr}},
+    {1, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {nullptr, &launch_skinny<DT_BF16>, &launch_skinny<DT_F16>}},
 };
 static constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -97,6 +103,44 @@ static bool needs_small_tile(int ma, int mb) {
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Load width (bytes) of the few-row kernel for these operands, or 0 when it
+// cannot run them: it needs M <= 64, both operands K-contiguous, and 32-bit
+// byte offsets over A and over 16 rows of B.
+static int skinny_width(int64_t m, int64_t k, int64_t sam, int64_t sak, int64_t sbn, int64_t sbk, int ma, int mb,
+                        int esz) {
+  if (m > kSkinnyMaxRows || sak != 1 || sbk != 1 || sam < 0 || sbn < 0 || sam >= kMaxBufferBytes ||
+      sbn >= kMaxBufferBytes)
+    return 0;
+  if (((m - 1) * sam + k) * esz + 16 >= kMaxBufferBytes || (15 * sbn + k) * esz + 16 >= kMaxBufferBytes) return 0;
+  if (ma == MODE_K && mb == MODE_K) return 16;
+  if ((ma == MODE_K || ma == MODE_K4) && (mb == MODE_K || mb == MODE_K4)) return 4;
+  return esz == 2 ? 2 : 0;
+}
+
+// Whether the shape heuristic prefers the few-row kernel (it runs whenever
+// skinny_width allows, if asked for by config id).  Each of its 8 waves
+// streams its share of K through a ring of kSkinnyDepth chunks, one memory
+// latency per ring round, and every workgroup (16 columns) reads all of A.
+// It beats the tiled kernels when a wave needs at most two rounds and either
+// A is at most one 16-row block (so reading it per workgroup is cheap) or,
+// with 16-byte loads, there are enough column groups to spread over the GPU;
+// at most three rounds for one row block.  Long K and narrow N go to the
+// tiled kernels (with split K).
+static bool skinny_preferred(int64_t m, int64_t n, int64_t k, int lw, int esz) {
+  if (lw == 0) return false;
+  const int64_t chunk = 64 / esz;  // K elements per chunk: 4 lane groups of 16 bytes
+  const int64_t per_wave = cdiv(cdiv(k, chunk), kSkinnyWaves);
+  const int64_t rounds = cdiv(per_wave, kSkinnyDepth);
+  if (m <= 16) return rounds <= 3;
+  return lw == 16 && rounds <= 2 && cdiv(n, 16) >= 48;
+}
+
+static int skinny_id(int dclass) {
+  for (int id = 0; id < kNumTiles; ++id)
+    if (kTiles[id].kind == KIND_SKINNY && kTiles[id].dclass == dclass) return id;
+  return -1;
+}
+
 // Shape heuristic behind FORGEML_CONFIG_AUTO: the largest tile that still
 // gives every one of the 256 CUs at least one workgroup (the smallest tile
 // otherwise; split K then adds workgroups).  Among equal areas, more waves
@@ -116,7 +160,7 @@ static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int ma,
   int best_waves = 0;
   for (int id = 0; id < kNumTiles; ++id) {
     const TileConfig& t = kTiles[id];
-    if (t.dclass != dclass) continue;
+    if (t.dclass != dclass || t.kind != KIND_TILED) continue;
     const int waves = t.wm * t.wn;
     if (waves > 4 && dclass == 1 && !all_k) continue;
     const int64_t area = (int64_t)t.bm * t.bn;
@@ -140,7 +184,7 @@ static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int ma,
 static constexpr int64_t kSplitBelowTiles = 128;
 static constexpr int64_t kSplitTargetWgs = 512;
 static constexpr int64_t kMinSliceStages = 4;
-static constexpr int64_t kMaxSplit = 16;
+static constexpr int64_t kMaxSplit = kMaxSplitK;
 
 struct SplitPlan {
   int splits;  // 1 = no split
@@ -151,7 +195,7 @@ static SplitPlan split_plan(const TileConfig& t, int64_t m, int64_t n, int64_t k
   const int64_t tiles = cdiv(m, t.bm) * cdiv(n, t.bn);
   const int64_t nk = cdiv(k * esz, kRowBytes);
   SplitPlan plan{1, (int)nk};
-  if (tiles >= kSplitBelowTiles) return plan;
+  if (t.kind != KIND_TILED || tiles >= kSplitBelowTiles) return plan;
   int64_t s = cdiv(kSplitTargetWgs, tiles);
   s = std::min(s, nk / kMinSliceStages);
   s = std::min(s, kMaxSplit);
@@ -185,17 +229,29 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
   out[0] = t.dclass;
   out[1] = t.bm;
   out[2] = t.bn;
-  out[3] = t.dclass == 0 ? kRowBytes / 4 : kRowBytes / 2;
   out[4] = t.wm * t.wn;
-  out[5] = 2;
+  if (t.kind == KIND_SKINNY) {
+    // block_k: K of one chunk (a 16-byte vector per lane, 4 lane groups);
+    // stages: chunks in flight per wave; LDS: the cross-wave reduction.
+    out[3] = t.dclass == 0 ? 16 : 32;
+    out[5] = kSkinnyDepth;
+    out[6] = 1;
+    out[7] = kSkinnyWaves * (kSkinnyMaxRows / 16) * 64 * 16;
+    return FORGEML_OK;
+  }
+  out[3] = t.dclass == 0 ? kRowBytes / 4 : kRowBytes / 2;
+  // Stages and LDS as built for K-contiguous operands (transposing loaders use two stages).
+  const int stages = (int64_t)t.bm * t.bn <= 64 * 64 ? 4 : 2;
+  out[5] = stages;
   out[6] = (int32_t)kMaxSplit;
-  out[7] = 2 * (t.bm + t.bn) * kRowBytes;
+  out[7] = stages * (t.bm + t.bn) * kRowBytes;
   return FORGEML_OK;
 }
 
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype) {
   if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "select_config: M, N, K must be positive");
+  if (m <= kSkinnyMaxRows && skinny_preferred(m, n, k, 16, esize_of(dtype))) return skinny_id(dclass_of(dtype));
   return select_config(m, n, k, dtype, MODE_K, MODE_K);
 }
 
@@ -218,19 +274,29 @@ int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t
   return most;
 }
 
-int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
-                     const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
-                     int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes, void* stream) {
-  g_last_error[0] = '\0';
-  if (a == nullptr || b == nullptr || c == nullptr) return set_error(FORGEML_EINVAL, "a, b and c must be non-NULL");
+}  // extern "C"
+
+namespace forgeml {
+
+// Everything forgeml_hip_gemm decides before a launch: argument checks, the
+// operands' load modes, the config, the K split and the workspace.
+struct LaunchPlan {
+  int config_id;
+  int combo;  // tiled: COMBO_*; few-row kernel: load width in bytes
+  SplitPlan split;
+  int64_t ws_need;
+  int64_t sam, sak, sbk, sbn;  // with size-1 dimensions' strides zeroed
+};
+
+static int plan_launch(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn, int64_t m,
+                       int64_t n, int64_t k, int32_t dtype, int32_t config_id, LaunchPlan& out) {
+  if (a == nullptr || b == nullptr) return set_error(FORGEML_EINVAL, "a and b must be non-NULL");
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "M, N, K must be positive (got %lld, %lld, %lld)",
                                                    (long long)m, (long long)n, (long long)k);
   if (m > INT_MAX || n > INT_MAX || k > INT_MAX || m * n > (int64_t)INT_MAX * 64)
     return set_error(FORGEML_EINVAL, "shape too large for this kernel family");
   if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
-  if (act < FORGEML_ACT_NONE || act > FORGEML_ACT_RELU) return set_error(FORGEML_EINVAL, "unknown activation %d", act);
-  if (sam < 0 || sak < 0 || sbk < 0 || sbn < 0 || sbi < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
-
+  if (sam < 0 || sak < 0 || sbk < 0 || sbn < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
   if (config_id != FORGEML_CONFIG_AUTO && (config_id < 0 || config_id >= kNumTiles))
     return set_error(FORGEML_ECONFIG, "config id %d out of range [0, %d)", config_id, kNumTiles);
 
@@ -245,17 +311,65 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   }
   const int ma = operand_mode(a, m, sam, sak, k, esz);
   const int mb = operand_mode(b, n, sbn, sbk, k, esz);
-  if (config_id == FORGEML_CONFIG_AUTO) config_id = select_config(m, n, k, dtype, ma, mb);
+  const int lw = skinny_width(m, k, sam, sak, sbn, sbk, ma, mb, esz);
+  if (config_id == FORGEML_CONFIG_AUTO)
+    config_id = skinny_preferred(m, n, k, lw, esz) ? skinny_id(dclass_of(dtype)) : select_config(m, n, k, dtype, ma, mb);
   const TileConfig& t = kTiles[config_id];
   if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
     return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
-  const int combo = combo_of(ma, mb, (int64_t)t.bm * t.bn <= kSmallTileArea);
-  const SplitPlan plan = split_plan(t, m, n, k, esz);
-  const int64_t ws_need = workspace_bytes_for(plan, m, n);
-  if (ws_need > 0) {
-    if (workspace == nullptr || workspace_bytes < ws_need)
+  if (t.kind == KIND_SKINNY && lw == 0)
+    return set_error(FORGEML_ECONFIG, "config %d (few-row kernel) needs M <= %d and K-contiguous A and B", config_id,
+                     kSkinnyMaxRows);
+  out.config_id = config_id;
+  out.combo = t.kind == KIND_SKINNY ? lw : combo_of(ma, mb, (int64_t)t.bm * t.bn <= kSmallTileArea);
+  out.split = split_plan(t, m, n, k, esz);
+  out.ws_need = workspace_bytes_for(out.split, m, n);
+  out.sam = sam;
+  out.sak = sak;
+  out.sbk = sbk;
+  out.sbn = sbn;
+  if (cdiv(m, t.bm) * cdiv(n, t.bn) * out.split.splits > INT_MAX)
+    return set_error(FORGEML_EINVAL, "too many output tiles");
+  return FORGEML_OK;
+}
+
+}  // namespace forgeml
+
+extern "C" {
+
+int forgeml_hip_gemm_plan(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn, int64_t m,
+                          int64_t n, int64_t k, int32_t dtype, int32_t config_id, int64_t* out) {
+  g_last_error[0] = '\0';
+  if (out == nullptr) return set_error(FORGEML_EINVAL, "gemm_plan: out is NULL");
+  LaunchPlan plan;
+  const int rc = plan_launch(a, sam, sak, b, sbk, sbn, m, n, k, dtype, config_id, plan);
+  if (rc != FORGEML_OK) return rc;
+  out[0] = plan.config_id;
+  out[1] = plan.split.splits;
+  out[2] = plan.ws_need;
+  out[3] = kTiles[plan.config_id].kind;
+  return FORGEML_OK;
+}
+
+int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
+                     const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
+                     int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  if (c == nullptr) return set_error(FORGEML_EINVAL, "a, b and c must be non-NULL");
+  if (act < FORGEML_ACT_NONE || act > FORGEML_ACT_RELU) return set_error(FORGEML_EINVAL, "unknown activation %d", act);
+  if (sbi < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
+  LaunchPlan plan;
+  const int rc = plan_launch(a, sam, sak, b, sbk, sbn, m, n, k, dtype, config_id, plan);
+  if (rc != FORGEML_OK) {
+    if (rc == FORGEML_EINVAL && (a == nullptr || b == nullptr)) return set_error(rc, "a, b and c must be non-NULL");
+    return rc;
+  }
+  const TileConfig& t = kTiles[plan.config_id];
+  if (plan.ws_need > 0) {
+    if (workspace == nullptr || workspace_bytes < plan.ws_need)
       return set_error(FORGEML_EWORKSPACE, "this shape splits K %d ways and needs %lld workspace bytes (got %lld)",
-                       plan.splits, (long long)ws_need, (long long)(workspace == nullptr ? 0 : workspace_bytes));
+                       plan.split.splits, (long long)plan.ws_need,
+                       (long long)(workspace == nullptr ? 0 : workspace_bytes));
     if (((uintptr_t)workspace & 15) != 0) return set_error(FORGEML_EWORKSPACE, "workspace must be 16-byte aligned");
   }
 
@@ -264,10 +378,10 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.b = (const char*)b;
   p.bias = (const char*)bias;
   p.c = (char*)c;
-  p.sam = sam;
-  p.sak = sak;
-  p.sbk = sbk;
-  p.sbn = sbn;
+  p.sam = plan.sam;
+  p.sak = plan.sak;
+  p.sbk = plan.sbk;
+  p.sbn = plan.sbn;
   p.sbi = sbi;
   p.m = (int)m;
   p.n = (int)n;
@@ -277,11 +391,10 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.tiles_m = (int)cdiv(m, t.bm);
   p.tiles_n = (int)cdiv(n, t.bn);
   p.group_m = p.tiles_m < 8 ? p.tiles_m : 8;
-  p.splits = plan.splits;
-  p.kslice = plan.kslice;
-  p.ws = ws_need > 0 ? (float*)workspace : nullptr;
-  if ((int64_t)p.tiles_m * p.tiles_n * plan.splits > INT_MAX) return set_error(FORGEML_EINVAL, "too many output tiles");
-  return t.launch[dtype](p, combo, (hipStream_t)stream);
+  p.splits = plan.split.splits;
+  p.kslice = plan.split.kslice;
+  p.ws = plan.ws_need > 0 ? (float*)workspace : nullptr;
+  return t.launch[dtype](p, plan.combo, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,5 +1,5 @@
 // fused_gemm_bf16.hip — instantiates the bf16 fused GEMM kernels of every tile
-// configuration (one translation unit per dtype so they build in parallel).
+// configuration and the few-row kernels (one translation unit per dtype so they build in parallel).
 #include "gemm_launch.hpp"
 #include "tile_table.hpp"
 
@@ -8,4 +8,5 @@ namespace forgeml {
   template int launch_tile<DT_BF16, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
 FORGEML_H16_TILES(FORGEML_INSTANTIATE)
 #undef FORGEML_INSTANTIATE
+template int launch_skinny<DT_BF16>(const GemmArgs&, int, hipStream_t);
 }  // namespace forgeml

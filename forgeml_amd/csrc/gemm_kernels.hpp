@@ -201,6 +201,7 @@ struct LoaderK {
   static constexpr int NWAVES = NT / 64;
   static constexpr int PER = (BLOCKS + NWAVES - 1) / NWAVES;
   static constexpr int kGlobalLoads = PER, kLdsWrites = 0;  // per thread per stage
+  static constexpr bool kExactPer = BLOCKS % NWAVES == 0;    // every wave issues PER DMAs
   __amdgpu_buffer_rsrc_t rsrc;
   int kbytes;
   uint32_t voff[PER];  // this lane's byte offset in stage 0, or out of range
@@ -256,6 +257,7 @@ struct LoaderK4 {
   static constexpr int NWAVES = NT / 64;
   static constexpr int PER = (BLOCKS + NWAVES - 1) / NWAVES;
   static constexpr int kGlobalLoads = PER, kLdsWrites = 0;
+  static constexpr bool kExactPer = BLOCKS % NWAVES == 0;
   __amdgpu_buffer_rsrc_t rsrc;
   int kbytes, ld_bytes, valid_rows;
   int lane_off;  // (L/32)*ld_bytes + (L%4)*4
@@ -306,6 +308,7 @@ struct LoaderMN {
   static constexpr int UNITS = UM * 8;
   static constexpr int PER = (UNITS + NT - 1) / NT;
   static constexpr int kGlobalLoads = PER * VEC, kLdsWrites = PER * VEC;
+  static constexpr bool kExactPer = false;
   __amdgpu_buffer_rsrc_t rsrc;
   int ld_bytes, k, valid;  // ld_bytes: bytes between consecutive K
   u32x4 v[PER][VEC];
@@ -378,6 +381,7 @@ struct LoaderG {
   static constexpr bool kStaged = PER <= 16;
   static constexpr int BATCH = 16;
   static constexpr int kGlobalLoads = kStaged ? PER : 0, kLdsWrites = kStaged ? PER : 0;
+  static constexpr bool kExactPer = false;
   static_assert(ELEMS % NT == 0 && NT % ROWS == 0 && NT % BKE == 0, "thread count must tile the stage");
   const char* safe;      // element (row0, 0): always inside the operand
   const char* p0;        // this thread's first element of stage 0
@@ -459,6 +463,15 @@ struct LoaderG {
   }
 };
 
+// LDS stage buffers of a kernel: small tiles whose operands both arrive by
+// DMA stream K with little MFMA work per stage, so they keep four stages in
+// flight (64 KiB, two workgroups per CU); the others use two.
+template <int BM, int BN, int AMODE, int BMODE>
+constexpr int lds_stages() {
+  return ((AMODE == MODE_K || AMODE == MODE_K4) && (BMODE == MODE_K || BMODE == MODE_K4) && BM * BN <= 64 * 64) ? 4
+                                                                                                              : 2;
+}
+
 template <int MODE, int DT, int ROWS, int NT>
 struct LoaderSel;
 template <int DT, int ROWS, int NT>
@@ -483,13 +496,16 @@ struct Frags {
   u32x4 b[TN];
 };
 
+// Reads are issued in the order the MFMAs (tm outer, tn inner) first use
+// them, so each MFMA waits only for its own operands.
 template <int TM, int TN>
 __device__ __forceinline__ void load_frags(Frags<TM, TN>& f, const char* lda, const char* ldb, int wr0, int wc0,
                                            int lr, int c) {
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) f.a[tm] = *(const u32x4*)(lda + lds_off(wr0 + tm * 32 + lr, c));
+  f.a[0] = *(const u32x4*)(lda + lds_off(wr0 + lr, c));
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) f.b[tn] = *(const u32x4*)(ldb + lds_off(wc0 + tn * 32 + lr, c));
+#pragma unroll
+  for (int tm = 1; tm < TM; ++tm) f.a[tm] = *(const u32x4*)(lda + lds_off(wr0 + tm * 32 + lr, c));
 }
 
 template <int DT, int TM, int TN>
@@ -515,19 +531,21 @@ __device__ __forceinline__ void mma_frags(const Frags<TM, TN>& f, f32x16 (&acc)[
 }
 
 // Instruction-order hints for the scheduler (masks: 0x008 MFMA, 0x100 LDS
-// read, 0x200 LDS write, 0x020 global read).  Each helper lays out one MFMA
-// step: NM MFMAs with the other instructions spread evenly between them, so
-// the single wave per SIMD keeps the matrix pipe fed while memory work issues.
+// read, 0x200 LDS write, 0x010 any global memory access; the DMA loads count
+// as both a global read and an LDS write, so they match only the generic
+// mask).  Each helper lays out one MFMA step: the next step's LDS reads all
+// follow the first MFMA, so they have the rest of the step to land, and the
+// LDS writes and global loads are spread evenly between the MFMAs so the
+// matrix pipe stays fed while memory work issues.
 template <int NM, int NR, int NW, int NG>
 __device__ __forceinline__ void sched_step() {
   // Each step is its own scheduling region (sched_barrier below), so the LDS
-  // reads placed between its MFMAs can only be the next step's fragments.
+  // reads placed in it can only be the next step's fragments.
 #pragma unroll
   for (int i = 0; i < NM; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    // Reads go first (one per MFMA) so they have the rest of the step to land.
     if constexpr (NR > 0) {
-      if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i == 0) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
     }
     if constexpr (NW > 0) {
 #pragma unroll
@@ -535,7 +553,7 @@ __device__ __forceinline__ void sched_step() {
     }
     if constexpr (NG > 0) {
 #pragma unroll
-      for (int j = (i * NG) / NM; j < ((i + 1) * NG) / NM; ++j) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      for (int j = (i * NG) / NM; j < ((i + 1) * NG) / NM; ++j) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -713,14 +731,6 @@ void fused_gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
 
-  // Software pipeline over K stages (4 MFMA steps of 32 bytes of K each):
-  //   step 0..2: LDS reads of step s+1 in flight while step s's MFMAs issue;
-  //   step 2:    registers holding stage kt+1 go to the other LDS buffer and
-  //              the global loads of stage kt+2 are issued;
-  //   step 3:    one barrier, then the next stage's step-0 reads overlap the
-  //              last MFMAs of this stage.
-  // The buffer written in step 2 was last read before the previous stage's
-  // barrier, and the buffer read after this barrier was written before it.
   const int lr = lane & 31, h = lane >> 5;
   using LA = typename LoaderSel<AMODE, DT, BM, NT>::type;
   using LB = typename LoaderSel<BMODE, DT, BN, NT>::type;
@@ -730,37 +740,47 @@ void fused_gemm_kernel(GemmArgs p) {
   constexpr int NG_DIRECT = (LA::kDirect ? LA::kGlobalLoads : 0) + (LB::kDirect ? LB::kGlobalLoads : 0);
   constexpr int NG_REG = (LA::kDirect ? 0 : LA::kGlobalLoads) + (LB::kDirect ? 0 : LB::kGlobalLoads);
   constexpr int NW = LA::kLdsWrites + LB::kLdsWrites;
+  constexpr int S = lds_stages<BM, BN, AMODE, BMODE>();
+  static_assert(S == 2 || (LA::kDirect && LB::kDirect && LA::kExactPer && LB::kExactPer),
+                "rings deeper than two stages count DMA instructions per wave exactly");
 
   // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage,
-  // two LDS buffers:
+  // S LDS buffers used as a ring:
   //   step 0-2: the LDS reads of step s+1 are in flight while step s's MFMAs
   //             issue;
-  //   step 2:   register loaders write stage kt+1 into the other buffer;
+  //   step 2:   register loaders write stage kt+1 into the next buffer;
   //   step 3:   wait until stage kt+1 has landed, one barrier, then the next
-  //             stage's step-0 reads, the DMA of stage kt+2 into the buffer
+  //             stage's step-0 reads, the DMA of stage kt+S into the buffer
   //             just released and the register loaders' global reads of stage
   //             kt+2 all overlap this stage's last MFMAs.
   // A buffer is refilled only after the barrier that follows its last read,
   // and read only after the barrier that follows its fill.  The DMA of a stage
-  // has four MFMA steps to land.  The body is branch-free: past the last stage
-  // every global read is out of range (zeros) and the extra LDS writes land in
-  // a buffer nothing reads.
+  // has S-1 stages of MFMAs to land; vector memory reads complete in issue
+  // order, so "at most (S-2) stages of DMA outstanding" means stage kt+1 has
+  // landed.  The body is branch-free: past the last stage every global read
+  // is out of range (zeros) and the extra LDS writes land in a buffer nothing
+  // reads.
   la.issue(kt0, smem);
   lb.issue(kt0, smem + BM * kRowBytes);
   la.commit(smem);
   lb.commit(smem + BM * kRowBytes);
-  if constexpr (LA::kDirect) la.issue(kt0 + 1, smem + STAGE);
-  if constexpr (LB::kDirect) lb.issue(kt0 + 1, smem + STAGE + BM * kRowBytes);
+#pragma unroll
+  for (int d = 1; d < S; ++d) {
+    if constexpr (LA::kDirect) la.issue(kt0 + d, smem + d * STAGE);
+    if constexpr (LB::kDirect) lb.issue(kt0 + d, smem + d * STAGE + BM * kRowBytes);
+  }
   if constexpr (!LA::kDirect) la.issue(kt0 + 1, nullptr);
   if constexpr (!LB::kDirect) lb.issue(kt0 + 1, nullptr);
-  if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stages kt0, kt0+1 landed
   __syncthreads();
   Frags<TM, TN> f0, f1;
   load_frags(f0, smem, smem + BM * kRowBytes, wr0, wc0, lr, h * 4);
+  int bi = 0;  // ring index of stage kt
   for (int it = 0; it < nks; ++it) {
     const int kt = kt0 + it;
-    char* cur = (it & 1) ? smem + STAGE : smem;
-    char* nxt = (it & 1) ? smem : smem + STAGE;
+    const int bn = bi + 1 == S ? 0 : bi + 1;
+    char* cur = smem + bi * STAGE;
+    char* nxt = smem + bn * STAGE;
     load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
     mma_frags<DT>(f0, acc);
     sched_step<NM, NR, 0, 0>();
@@ -772,15 +792,16 @@ void fused_gemm_kernel(GemmArgs p) {
     if constexpr (!LB::kDirect) lb.commit(nxt + BM * kRowBytes);
     mma_frags<DT>(f0, acc);
     sched_step<NM, NR, NW, 0>();
-    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): stage kt+1 landed
+    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stage kt+1 landed
     __syncthreads();
     load_frags(f0, nxt, nxt + BM * kRowBytes, wr0, wc0, lr, h * 4);
-    if constexpr (LA::kDirect) la.issue(kt + 2, cur);
-    if constexpr (LB::kDirect) lb.issue(kt + 2, cur + BM * kRowBytes);
+    if constexpr (LA::kDirect) la.issue(kt + S, cur);
+    if constexpr (LB::kDirect) lb.issue(kt + S, cur + BM * kRowBytes);
     if constexpr (!LA::kDirect) la.issue(kt + 2, nullptr);
     if constexpr (!LB::kDirect) lb.issue(kt + 2, nullptr);
     mma_frags<DT>(f1, acc);
     sched_step<NM, NR, 0, NG_DIRECT + NG_REG>();
+    bi = bn;
   }
   __syncthreads();
 
@@ -812,6 +833,8 @@ void fused_gemm_kernel(GemmArgs p) {
 // Split-K epilogue: C = act(rnd(rnd(sum_z ws[z]) + bias)), the slices summed
 // in order z = 0, 1, ... so results do not depend on scheduling.  Each thread
 // owns 4 consecutive elements of C (row-major, flattened).
+constexpr int kMaxSplitK = 16;  // most K slices a GEMM is split into
+
 struct ReduceArgs {
   const float* ws;
   const char* bias;
@@ -828,14 +851,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs p) {
   const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (e0 >= p.mn) return;
   const int cnt = p.mn - e0 < 4 ? (int)(p.mn - e0) : 4;
+  // Every slice's values are loaded before the first add, so the loads are
+  // in flight together rather than one latency per slice.
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (p.vec) {
-    for (int z = 0; z < p.splits; ++z) {
-      const float4 w = *(const float4*)(p.ws + (int64_t)z * p.mn + e0);
-      v[0] += w.x;
-      v[1] += w.y;
-      v[2] += w.z;
-      v[3] += w.w;
+    float4 w[kMaxSplitK];
+#pragma unroll
+    for (int z = 0; z < kMaxSplitK; ++z)
+      if (z < p.splits) w[z] = *(const float4*)(p.ws + (int64_t)z * p.mn + e0);
+#pragma unroll
+    for (int z = 0; z < kMaxSplitK; ++z) {
+      if (z < p.splits) {
+        v[0] += w[z].x;
+        v[1] += w[z].y;
+        v[2] += w[z].z;
+        v[3] += w[z].w;
+      }
     }
   } else {
     for (int z = 0; z < p.splits; ++z)

@@ -6,6 +6,7 @@
 #include <atomic>
 
 #include "gemm_kernels.hpp"
+#include "skinny_kernels.hpp"
 
 namespace forgeml {
 
@@ -58,7 +59,7 @@ int launch_reduce(const GemmArgs& p, hipStream_t stream) {
 template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
 int launch_one(const GemmArgs& p, hipStream_t stream) {
   constexpr int NT = WM * WN * 64;
-  constexpr int LDS = 2 * (BM + BN) * kRowBytes;
+  constexpr int LDS = lds_stages<BM, BN, AMODE, BMODE>() * (BM + BN) * kRowBytes;
   const void* fn = reinterpret_cast<const void*>(&fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE>);
   if constexpr (LDS > 65536) {
     // Above 64 KiB the dynamic LDS limit must be raised once per device
@@ -100,12 +101,45 @@ int launch_tile(const GemmArgs& p, int combo, hipStream_t stream) {
   }
 }
 
+// Few-row kernel: TM = ceil(M / 16) row blocks, `lw` the load width in bytes
+// (16, 4 or 2) both operands' alignment allows.
+template <int DT, int TM, int LW>
+int launch_skinny_one(const GemmArgs& p, hipStream_t stream) {
+  hipLaunchKernelGGL((skinny_gemm_kernel<DT, TM, LW>), dim3((unsigned)((p.n + 15) / 16)), dim3(kSkinnyThreads), 0,
+                     stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(-3, "kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+template <int DT, int LW>
+int launch_skinny_lw(const GemmArgs& p, hipStream_t stream) {
+  switch ((p.m + 15) / 16) {
+    case 1: return launch_skinny_one<DT, 1, LW>(p, stream);
+    case 2: return launch_skinny_one<DT, 2, LW>(p, stream);
+    case 3: return launch_skinny_one<DT, 3, LW>(p, stream);
+    default: return launch_skinny_one<DT, 4, LW>(p, stream);
+  }
+}
+
+template <int DT>
+int launch_skinny(const GemmArgs& p, int lw, hipStream_t stream) {
+  if (lw == 16) return launch_skinny_lw<DT, 16>(p, stream);
+  if constexpr (DT != DT_F32) {
+    if (lw == 2) return launch_skinny_lw<DT, 2>(p, stream);
+  }
+  return launch_skinny_lw<DT, 4>(p, stream);
+}
+
 using TileLauncher = int (*)(const GemmArgs&, int, hipStream_t);
+
+enum : int { KIND_TILED = 0, KIND_SKINNY = 1 };
 
 // Tile table, defined in fused_gemm_abi.hip.
 struct TileConfig {
   int dclass;  // 0 = fp32, 1 = 16-bit
   int bm, bn, wm, wn;
+  int kind;    // KIND_TILED, or KIND_SKINNY (bm = most rows, bn = columns per workgroup)
   TileLauncher launch[3];  // indexed by DT_*; null where not built
 };
 

@@ -50,12 +50,22 @@ DEFAULT_CONFIG = KernelConfig()
 
 # The library's tile table, in config-id order (forgeml_amd/csrc/tile_table.hpp).
 # A CPU test checks it against forgeml_hip_config_info.
-_FP32_TILES = ((128, 128, 4), (64, 64, 4), (256, 128, 8))
-_H16_TILES = ((256, 256, 4), (128, 128, 4), (64, 64, 4), (256, 256, 8))
+# (block_m, block_n, waves, LDS stages); the 64x64 tiles keep four stages in
+# flight when both operands are K-contiguous.
+_FP32_TILES = ((128, 128, 4, 2), (64, 64, 4, 4), (256, 128, 8, 2))
+_H16_TILES = ((256, 256, 4, 2), (128, 128, 4, 2), (64, 64, 4, 4), (256, 256, 8, 2))
+# The few-row kernels come last: up to 64 rows, 16 columns per workgroup, 8
+# waves splitting K in chunks of 16 fp32 / 32 16-bit elements, 4 chunks in
+# flight per wave.  They run only K-contiguous A and B.
+SKINNY_FP32 = KernelConfig(64, 16, 16, 8, 4)
+SKINNY_H16 = KernelConfig(64, 16, 32, 8, 4)
 CANDIDATES: tuple[KernelConfig, ...] = tuple(
-    [KernelConfig(bm, bn, 32, w, 2) for bm, bn, w in _FP32_TILES]
-    + [KernelConfig(bm, bn, 64, w, 2) for bm, bn, w in _H16_TILES]
+    [KernelConfig(bm, bn, 32, w, st) for bm, bn, w, st in _FP32_TILES]
+    + [KernelConfig(bm, bn, 64, w, st) for bm, bn, w, st in _H16_TILES]
+    + [SKINNY_FP32, SKINNY_H16]
 )
+# dtype class of each candidate: 0 = fp32, 1 = bf16/fp16.
+_CANDIDATE_CLASS = tuple([0] * len(_FP32_TILES) + [1] * len(_H16_TILES) + [0, 1])
 _CONFIG_IDS = {cfg: i for i, cfg in enumerate(CANDIDATES)}
 
 _DTYPES = {torch.float16, torch.bfloat16, torch.float32}
@@ -67,8 +77,8 @@ TARGET_ARCH = "gfx950"
 
 def candidates(dtype: torch.dtype) -> tuple[KernelConfig, ...]:
     """Tile configurations built for ``dtype`` (the autotuner's search space)."""
-    block_k = 32 if dtype == torch.float32 else 64
-    return tuple(c for c in CANDIDATES if c.block_k == block_k)
+    dclass = 0 if dtype == torch.float32 else 1
+    return tuple(c for c, k in zip(CANDIDATES, _CANDIDATE_CLASS) if k == dclass)
 
 
 def _device_arch(device: torch.device) -> str:
@@ -162,10 +172,35 @@ def launch(
 
 
 def workspace_for(m: int, n: int, k: int, dtype: torch.dtype, cid: int, device: torch.device) -> torch.Tensor | None:
+    """A workspace large enough for any operand layout of this shape (None if none splits K)."""
     nbytes = _native.load().forgeml_hip_gemm_workspace_size(m, n, k, _DTYPE_CODES[dtype], cid)
     if nbytes < 0:
         raise GraphError(f"workspace_size failed: {_native.last_error()}")
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+KIND_NAMES = ("tiled", "few-row")
+
+
+def plan(a: torch.Tensor, b: torch.Tensor, config: KernelConfig = DEFAULT_CONFIG) -> dict:
+    """What ``matmul(a, b, config=config)`` runs: config, K slices, workspace bytes, kernel kind."""
+    cid = _check_config(config, a.dtype)
+    m, k = a.shape
+    n = b.shape[1]
+    out = (ctypes.c_int64 * 4)()
+    rc = _native.load().forgeml_hip_gemm_plan(
+        a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1),
+        m, n, k, _DTYPE_CODES[a.dtype], cid, out,
+    )
+    if rc != _native.OK:
+        raise GraphError(f"forgeml_hip_gemm_plan failed ({rc}): {_native.last_error()}")
+    return {
+        "config": CANDIDATES[out[0]],
+        "config_id": int(out[0]),
+        "k_splits": int(out[1]),
+        "workspace_bytes": int(out[2]),
+        "kernel": KIND_NAMES[out[3]],
+    }
 
 
 def matmul(
@@ -234,7 +269,8 @@ def matmul(
             if src is not None and src.untyped_storage().data_ptr() == out_ptr:
                 raise GraphError("out must not share storage with inputs")
     with torch.cuda.device(a.device):
-        ws = workspace_for(m, n, k, a.dtype, cid, a.device)
+        nbytes = plan(a, b, config)["workspace_bytes"]
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
         return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws)
 
 

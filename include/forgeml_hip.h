@@ -89,15 +89,31 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
                      void* workspace, int64_t workspace_bytes,
                      void* stream);
 
-/* Bytes of workspace forgeml_hip_gemm needs for this shape and config
- * (0 for configs that do not split K).  Negative on bad arguments.
- * No reference counterpart: the reference has no split-K kernel. */
+/* What forgeml_hip_gemm would run for these operands, without launching:
+ *   out[0]  the config id (resolved when config_id is FORGEML_CONFIG_AUTO)
+ *   out[1]  the number of K slices (1 = K is not split)
+ *   out[2]  workspace bytes the call needs (0 when K is not split)
+ *   out[3]  kernel kind: 0 = tiled, 1 = few-row (M <= 64)
+ * Pointers are used only for their alignment.  Returns FORGEML_OK or the
+ * error forgeml_hip_gemm would return for them.  No reference counterpart:
+ * the reference's launcher has no split-K workspace to size. */
+int forgeml_hip_gemm_plan(const void* a, int64_t sam, int64_t sak,
+                          const void* b, int64_t sbk, int64_t sbn,
+                          int64_t m, int64_t n, int64_t k,
+                          int32_t dtype, int32_t config_id, int64_t* out);
+
+/* Bytes of workspace forgeml_hip_gemm needs for this shape and config, for
+ * any operand layout (an upper bound when config_id is FORGEML_CONFIG_AUTO;
+ * forgeml_hip_gemm_plan gives the exact figure for given operands).  0 when
+ * no layout splits K; negative on bad arguments.  No reference counterpart:
+ * the reference has no split-K kernel. */
 int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k,
                                         int32_t dtype, int32_t config_id);
 
 /* The config id FORGEML_CONFIG_AUTO resolves to for this shape when both
- * operands are K-contiguous (forgeml_hip_gemm also weighs the layout).
- * Counterpart of DEFAULT_CONFIG (src/forgeml/kernels.py:21). */
+ * operands are K-contiguous with 16-byte aligned rows (forgeml_hip_gemm also
+ * weighs the actual layout).  Counterpart of DEFAULT_CONFIG
+ * (src/forgeml/kernels.py:21). */
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype);
 
 /* Number of entries in the tile table.  Counterpart of
@@ -115,7 +131,7 @@ const char* forgeml_hip_last_error(void);
 /* ABI version of this header; bumped on any signature change. */
 int forgeml_hip_abi_version(void);
 
-#define FORGEML_HIP_ABI_VERSION 1
+#define FORGEML_HIP_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

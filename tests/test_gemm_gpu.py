@@ -176,6 +176,11 @@ def test_every_config_and_layout(gpu, dtype):
             what = f"{dtype} config={config} layout={name} seed={seed}"
             _say(what)
             a_d, b_d = make_a(gpu), make_b(gpu)
+            if config in (kernels.SKINNY_FP32, kernels.SKINNY_H16):
+                # The few-row kernel takes at most 64 rows: an explicit request is refused.
+                with pytest.raises(GraphError, match="few-row"):
+                    kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
+                continue
             got = kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
             _gate(got, expected, k, what)
 
@@ -195,7 +200,8 @@ def test_unaligned_k_layouts(gpu, dtype, m, n, k):
     expected = reference_cpu(a, b_nt, bias, "gelu")
     a_d, bias_d = a.to(gpu), bias.to(gpu)
     layouts = {"nt": to_gpu(b_nt, gpu), "nn": b_nt.contiguous().to(gpu)}
-    for config in (kernels.DEFAULT_CONFIG,) + kernels.candidates(dtype):
+    tiled = tuple(c for c in kernels.candidates(dtype) if c not in (kernels.SKINNY_FP32, kernels.SKINNY_H16))
+    for config in (kernels.DEFAULT_CONFIG,) + tiled:
         for name, b_d in layouts.items():
             what = f"M={m} N={n} K={k} {dtype} B={name} config={config} seed={seed}"
             _say(what)
@@ -207,7 +213,8 @@ def test_unaligned_k_layouts(gpu, dtype, m, n, k):
 def test_split_k_epilogues(gpu, dtype):
     m, n, k = 5, 640, 3000
     seed = case_seed("split_k", dtype)
-    a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+    # B stored [K, N]: the tiled kernels run it (the few-row kernel takes W^T).
+    a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout="nn")
     ws = kernels.workspace_for(m, n, k, dtype, -1, gpu)
     assert ws is not None, "this skinny shape is expected to split K"
     a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
@@ -225,7 +232,7 @@ def test_split_k_epilogues(gpu, dtype):
 
 def test_split_k_workspace_is_checked(gpu):
     m, n, k = 1, 768, 4096
-    a, b, _ = gemm_inputs(m, n, k, torch.float32, seed=case_seed("ws_check"), bias=False)
+    a, b, _ = gemm_inputs(m, n, k, torch.float32, seed=case_seed("ws_check"), bias=False, b_layout="nn")
     a_d, b_d = a.to(gpu), to_gpu(b, gpu)
     out = torch.empty(m, n, device=gpu)
     _say("split-K workspace check")
@@ -234,6 +241,55 @@ def test_split_k_workspace_is_checked(gpu):
     ws = kernels.workspace_for(m, n, k, torch.float32, -1, gpu)
     kernels.launch(a_d, b_d, None, out, act=0, config_id=-1, workspace=ws)
     _gate(out, reference_cpu(a, b), k, "split-K explicit workspace")
+
+
+# -- the few-row kernel (M <= 64, K-contiguous A and B) -------------------------
+#
+# K values cover 16-byte rows (768, 1024), 4-byte rows (odd fp32 K 1531; 16-bit
+# K = 2 mod 8: 1002) and 2-byte rows (odd 16-bit K 1531); M covers 1..4 row
+# blocks of 16 and N edges of the 16-column workgroups.
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+@pytest.mark.parametrize("k", [8, 768, 1002, 1531])
+def test_few_row_kernel(gpu, dtype, k):
+    config = kernels.SKINNY_FP32 if dtype == torch.float32 else kernels.SKINNY_H16
+    for m in (1, 5, 16, 17, 33, 64):
+        for n in (16, 40, 3000):
+            seed = case_seed("few_row", m, n, k, dtype)
+            a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+            a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+            for activation, approximate in (("gelu", "none"), ("gelu", "tanh"), ("none", "none"), ("relu", "none")):
+                what = f"few-row M={m} N={n} K={k} {dtype} act={activation}/{approximate} seed={seed}"
+                _say(what)
+                got = kernels.matmul(a_d, b_d, bias_d, activation=activation, approximate=approximate, config=config)
+                _gate(got, reference_cpu(a, b, bias, activation, approximate), k, what)
+            got = kernels.matmul(a_d, b_d, config=config)
+            _gate(got, reference_cpu(a, b), k, f"few-row M={m} N={n} K={k} {dtype} no bias, explicit config")
+
+
+def test_few_row_kernel_strided_rows_and_determinism(gpu):
+    # A rows padded to a longer stride, bias strided: still K-contiguous.
+    m, n, k = 24, 200, 520
+    g = torch.Generator().manual_seed(case_seed("few_row_strided"))
+    a_full = torch.randn(m, k + 40, generator=g) * k ** -0.25
+    w = torch.randn(n, k, generator=g) * k ** -0.25
+    bias_full = torch.rand(2 * n, generator=g) * 0.2 - 0.1
+    a = a_full[:, :k]
+    expected = reference_cpu(a, w.t(), bias_full[::2], "gelu")
+    a_d = a_full.to(gpu)[:, :k]
+    b_d = w.to(gpu).t()
+    bias_d = bias_full.to(gpu)[::2]
+    _say("few-row strided rows")
+    cfg = kernels.SKINNY_FP32
+    assert kernels.plan(a_d, b_d, cfg)["kernel"] == "few-row"
+    got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=cfg)
+    _gate(got, expected, k, "few-row strided rows")
+    assert torch.equal(got, kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=cfg))
+    # Chosen by the shape heuristic for one row and a short K.
+    a1 = a_d[:1]
+    assert kernels.plan(a1, b_d)["kernel"] == "few-row"
+    _gate(kernels.matmul(a1, b_d, bias_d, activation="gelu"), reference_cpu(a[:1], w.t(), bias_full[::2], "gelu"), k,
+          "few-row auto")
 
 
 def test_deterministic(gpu):

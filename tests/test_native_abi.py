@@ -36,8 +36,13 @@ def test_config_table_matches_python_candidates():
     for info, cfg in zip(table, kernels.CANDIDATES):
         dclass, bm, bn, bk, waves, stages, split, lds = info
         assert (bm, bn, bk, waves, stages) == (cfg.block_m, cfg.block_n, cfg.block_k, cfg.num_waves, cfg.num_stages)
-        assert dclass == (0 if cfg.block_k == 32 else 1) and split == 16
-        assert lds == 2 * (bm + bn) * 128 and lds <= 160 * 1024
+        assert cfg in kernels.candidates(torch.float32 if dclass == 0 else torch.bfloat16)
+        if cfg in (kernels.SKINNY_FP32, kernels.SKINNY_H16):
+            # Few-row kernel: chunks of one 16-byte vector per lane, 4 lane groups.
+            assert bk * (4 if dclass == 0 else 2) == 64 and split == 1 and lds == 8 * 4 * 64 * 16
+        else:
+            assert bk * (4 if dclass == 0 else 2) == 128 and split == 16
+            assert lds == stages * (bm + bn) * 128 and lds <= 160 * 1024
 
 
 def test_host_side_errors_without_launching():
@@ -107,10 +112,63 @@ def test_split_k_needs_workspace():
     m, n, k = 1, 768, 4096
     need = lib.forgeml_hip_gemm_workspace_size(m, n, k, _native.DTYPE_F32, -1)
     assert need > 0
-    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, None, 0, None)
+    # B stored [K, N] (N-contiguous): the tiled kernels run it, splitting K.
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, n, 1, None, 0, dummy, m, n, k, 0, 1, -1, None, 0, None)
     assert rc == _native.EWORKSPACE and "workspace" in _native.last_error()
-    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, dummy, need - 4, None)
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, n, 1, None, 0, dummy, m, n, k, 0, 1, -1, dummy, need - 4, None)
     assert rc == _native.EWORKSPACE
-    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, 1, k, None, 0, dummy, m, n, k, 0, 1, -1, ctypes.c_void_p(20), need,
+    rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, n, 1, None, 0, dummy, m, n, k, 0, 1, -1, ctypes.c_void_p(20), need,
                               None)
     assert rc == _native.EWORKSPACE and "aligned" in _native.last_error()
+
+
+def test_few_row_kernel_selection():
+    lib = _native.load()
+    table = _native.config_table()
+    skinny = [i for i, info in enumerate(table) if info[2] == 16]
+    assert len(skinny) == 2 and {table[i][0] for i in skinny} == {0, 1}
+    for dtype in (_native.DTYPE_F32, _native.DTYPE_BF16):
+        # Few rows, K streamed in at most two rounds per wave: the few-row kernel.
+        assert lib.forgeml_hip_select_config(1, 3072, 1024, dtype) in skinny
+        assert lib.forgeml_hip_select_config(48, 3072, 1024, dtype) in skinny
+        # More than 64 rows, a long K, or too few column groups: the tiled kernels.
+        assert lib.forgeml_hip_select_config(65, 3072, 1024, dtype) not in skinny
+        assert lib.forgeml_hip_select_config(64, 4096, 4096, dtype) not in skinny
+        assert lib.forgeml_hip_select_config(64, 512, 2048, dtype) not in skinny
+    # The few-row kernel needs K-contiguous A and B and at most 64 rows.
+    dummy = ctypes.c_void_p(16)
+    f32_skinny = next(i for i in skinny if table[i][0] == 0)
+    rc = lib.forgeml_hip_gemm(dummy, 64, 1, dummy, 64, 1, None, 0, dummy, 8, 64, 64, 0, 0, f32_skinny, None, 0, None)
+    assert rc == _native.ECONFIG and "few-row" in _native.last_error()
+    rc = lib.forgeml_hip_gemm(dummy, 64, 1, dummy, 1, 64, None, 0, dummy, 65, 64, 64, 0, 0, f32_skinny, None, 0, None)
+    assert rc == _native.ECONFIG
+
+
+def test_gemm_plan_reports_what_runs():
+    lib = _native.load()
+    out = (ctypes.c_int64 * 4)()
+    dummy = ctypes.c_void_p(256)  # only its alignment is looked at
+    f32 = _native.DTYPE_F32
+
+    def plan(m, n, k, sam, sak, sbk, sbn, dtype=f32, cid=-1, a=dummy, b=dummy):
+        rc = lib.forgeml_hip_gemm_plan(a, sam, sak, b, sbk, sbn, m, n, k, dtype, cid, out)
+        return rc, list(out)
+
+    # One row, B = W^T with 16-byte rows: the few-row kernel, no split.
+    rc, (cid, splits, ws, kind) = plan(1, 3072, 1024, 1024, 1, 1, 1024)
+    assert rc == 0 and kind == 1 and splits == 1 and ws == 0
+    # The same with B stored [K, N]: a tiled kernel splitting K over a workspace.
+    rc, (cid, splits, ws, kind) = plan(1, 768, 4096, 4096, 1, 768, 1)
+    assert rc == 0 and kind == 0 and splits > 1 and ws == splits * 1 * 768 * 4
+    assert ws <= lib.forgeml_hip_gemm_workspace_size(1, 768, 4096, f32, -1)
+    # A large square GEMM: the shape heuristic's tile, no split.
+    rc, (cid, splits, ws, kind) = plan(4096, 4096, 4096, 4096, 1, 1, 4096)
+    assert rc == 0 and kind == 0 and splits == 1 and ws == 0
+    assert cid == lib.forgeml_hip_select_config(4096, 4096, 4096, f32)
+    # Odd fp32 K and 33 rows: 4-byte rows go to the tiled kernels.
+    rc, (cid, splits, ws, kind) = plan(33, 3000, 1531, 1531, 1, 1, 1531)
+    assert rc == 0 and kind == 0
+    # Errors are the launch's errors.
+    rc, _ = plan(8, 64, 64, 64, 1, -1, 1)  # negative stride
+    assert rc == _native.EINVAL
+    assert lib.forgeml_hip_gemm_plan(dummy, 4, 1, dummy, 1, 4, 4, 4, 4, f32, -1, None) == _native.EINVAL
