@@ -102,7 +102,104 @@ class CompiledModel:
                 n = alloc.size_bytes // node.spec.dtype.itemsize
                 self._views[node.name] = self._slots[alloc.slot][:n].view(node.spec.shape)
         self._kernel_layout_constants()
-        self._steps = [(node, self._make_step(node)) for node in self.graph.nodes]
+        self._build_steps()
+
+    def _build_steps(self) -> None:
+        """Closures per node, with hip GEMMs fused with the residual add after them."""
+        object.__setattr__(self, "fused_residuals", self._plan_residual_fusions())
+        fused_adds = {add: carried for add, _view, _r, carried in self.fused_residuals.values()}
+        steps = []
+        for node in self.graph.nodes:
+            inputs = tuple(node.inputs)
+            if node.name in self.fused_residuals:
+                add_name, _view, residual, _carried = self.fused_residuals[node.name]
+                run = self._make_fused_residual_step(node, add_name)
+                inputs = inputs + (residual,)
+            elif node.name in fused_adds:
+                # The add was done in the GEMM's epilogue: pass its result on.
+                pos = node.inputs.index(fused_adds[node.name])
+                run = (lambda p: (lambda args: args[p]))(pos)
+            else:
+                run = self._make_step(node)
+            steps.append((node, run, inputs))
+        object.__setattr__(self, "_steps", steps)
+
+    def _plan_residual_fusions(self) -> dict[str, tuple[str, str | None, str, str]]:
+        """GEMM nodes whose result only feeds an ``add`` (optionally through one
+        reshape) immediately after them in the schedule.
+
+        The reference runs the GEMM, then the add as a second kernel
+        (src/forgeml/compiler.py:93-98); here the GEMM's epilogue adds the other
+        operand and writes the add's destination directly, and the add node
+        passes that result on.  Conditions: the GEMM is hip-planned and not a
+        graph output; the chain is adjacent in the schedule, so nothing runs in
+        between; shapes match without broadcasting; and the add's slot (if it
+        has one) holds none of the GEMM's inputs or the other operand, so the
+        early write clobbers nothing.  Returns gemm -> (add, reshape or None,
+        residual, the add's input that carries the GEMM result).
+        """
+        nodes = self.graph.nodes
+        index = {n.name: i for i, n in enumerate(nodes)}
+        producer = {n.name: n for n in nodes}
+        consumers: dict[str, list] = {}
+        for n in nodes:
+            for src in n.inputs:
+                consumers.setdefault(src, []).append(n)
+        specs = self.graph.specs()
+
+        def root_slot(name: str):
+            while name in producer and producer[name].op in VIEW_LIKE_OPS:
+                name = producer[name].inputs[0]
+            alloc = self.memory_plan.allocations.get(name)
+            return None if alloc is None else alloc.slot
+
+        fusions = {}
+        for i, node in enumerate(nodes):
+            if node.op not in kernels.GEMM_OPS or self.kernel_plan.get(node.name) != "hip":
+                continue
+            if node.name in self._outputs or len(consumers.get(node.name, [])) != 1:
+                continue
+            view, nxt, carried = None, consumers[node.name][0], node.name
+            if nxt.op == "reshape":
+                if index[nxt.name] != i + 1 or nxt.name in self._outputs or len(consumers.get(nxt.name, [])) != 1:
+                    continue
+                view, carried, nxt = nxt, nxt.name, consumers[nxt.name][0]
+            if nxt.op != "add" or index[nxt.name] != i + (2 if view else 1) or len(nxt.inputs) != 2:
+                continue
+            others = [x for x in nxt.inputs if x != carried]
+            if len(others) != 1:
+                continue
+            residual = others[0]
+            dtype = node.spec.dtype
+            if (
+                tuple(specs[residual].shape) != tuple(nxt.spec.shape)
+                or tuple(specs[carried].shape) != tuple(nxt.spec.shape)
+                or specs[residual].dtype != dtype
+                or nxt.spec.dtype != dtype
+            ):
+                continue
+            dest = root_slot(nxt.name) if nxt.name not in self._outputs else None
+            if dest is not None and any(root_slot(x) == dest for x in (*node.inputs, residual)):
+                continue
+            fusions[node.name] = (nxt.name, None if view is None else view.name, residual, carried)
+        return fusions
+
+    def _make_fused_residual_step(self, node, add_name: str):
+        add_node = next(n for n in self.graph.nodes if n.name == add_name)
+        to_output = add_name in self._outputs
+        slot_view = None if to_output else self._views[add_name]
+        m, n = node.spec.shape
+        spec = add_node.spec
+
+        def run(args):
+            *gemm_args, residual = args
+            if to_output:
+                dest = torch.empty(spec.shape, dtype=spec.dtype, device=gemm_args[0].device)
+            else:
+                dest = slot_view
+            return self._run_hip(node, tuple(gemm_args), dest.view(m, n), residual=residual.reshape(m, n))
+
+        return run
 
     def _kernel_layout_constants(self) -> None:
         """Store GEMM weights of hip-planned nodes K-contiguous.
@@ -128,7 +225,7 @@ class CompiledModel:
         # A new kernel plan changes dispatch, so rebuild the step closures.
         if name == "kernel_plan" and "_views" in self.__dict__:
             self._kernel_layout_constants()
-            object.__setattr__(self, "_steps", [(n, self._make_step(n)) for n in self.graph.nodes])
+            self._build_steps()
 
     def _make_step(self, node):
         on_hip = self.kernel_plan.get(node.name) == "hip"
@@ -179,8 +276,8 @@ class CompiledModel:
         outputs = self._outputs
         remaining = dict(self._uses_template)
         with torch.inference_mode():
-            for node, run in self._steps:
-                values[node.name] = run(tuple(values[i] for i in node.inputs))
+            for node, run, inputs in self._steps:
+                values[node.name] = run(tuple(values[i] for i in inputs))
                 for src in node.inputs:
                     if src in remaining:
                         remaining[src] -= 1
@@ -203,17 +300,21 @@ class CompiledModel:
         except Exception as e:  # noqa: BLE001
             raise GraphError(f"node {node.name!r} ({node.op}) execution failed: {e}") from e
 
-    def _run_hip(self, node, args: tuple[torch.Tensor, ...], out: torch.Tensor | None) -> torch.Tensor:
+    def _run_hip(self, node, args: tuple[torch.Tensor, ...], out: torch.Tensor | None,
+                 residual: torch.Tensor | None = None) -> torch.Tensor:
         config = self.kernel_configs.get(node.name, DEFAULT_CONFIG)
         bias = args[2] if len(args) == 3 else None
+        # The residual keyword is passed only when fused, so a replacement
+        # kernels.matmul with the reference's signature keeps working otherwise.
+        extra = {} if residual is None else {"residual": residual}
         if node.op == "matmul":
-            return kernels.matmul(args[0], args[1], config=config, out=out)
+            return kernels.matmul(args[0], args[1], config=config, out=out, **extra)
         if node.op == "linear":
-            return kernels.matmul(args[0], args[1], bias, config=config, out=out)
+            return kernels.matmul(args[0], args[1], bias, config=config, out=out, **extra)
         if node.op == "fused_linear_gelu":
             return kernels.matmul(
                 args[0], args[1], bias, activation="gelu",
-                approximate=node.attrs.get("approximate", "none"), config=config, out=out,
+                approximate=node.attrs.get("approximate", "none"), config=config, out=out, **extra,
             )
         raise GraphError(f"no hip kernel for op {node.op!r}")
 

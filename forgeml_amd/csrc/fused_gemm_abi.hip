@@ -351,19 +351,31 @@ int forgeml_hip_gemm_plan(const void* a, int64_t sam, int64_t sak, const void* b
   return FORGEML_OK;
 }
 
-int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
-                     const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
-                     int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace forgeml {
+
+static int gemm_impl(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn, const void* bias,
+                     int64_t sbi, void* c, const void* res, int64_t srm, int64_t srn, int64_t m, int64_t n, int64_t k,
+                     int32_t dtype, int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes,
+                     void* stream) {
   g_last_error[0] = '\0';
-  if (c == nullptr) return set_error(FORGEML_EINVAL, "a, b and c must be non-NULL");
+  if (a == nullptr || b == nullptr || c == nullptr) return set_error(FORGEML_EINVAL, "a, b and c must be non-NULL");
   if (act < FORGEML_ACT_NONE || act > FORGEML_ACT_RELU) return set_error(FORGEML_EINVAL, "unknown activation %d", act);
-  if (sbi < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
+  if (sbi < 0 || srm < 0 || srn < 0) return set_error(FORGEML_EINVAL, "negative strides are not supported");
   LaunchPlan plan;
   const int rc = plan_launch(a, sam, sak, b, sbk, sbn, m, n, k, dtype, config_id, plan);
-  if (rc != FORGEML_OK) {
-    if (rc == FORGEML_EINVAL && (a == nullptr || b == nullptr)) return set_error(rc, "a, b and c must be non-NULL");
-    return rc;
+  if (rc != FORGEML_OK) return rc;
+  if (res != nullptr && res != c) {
+    // The residual may be C itself (each element is read, then written, by one
+    // thread) but must not partly overlap it.
+    const int esz = esize_of(dtype);
+    const uintptr_t r0 = (uintptr_t)res, r1 = r0 + (uintptr_t)(((m - 1) * srm + (n - 1) * srn + 1) * esz);
+    const uintptr_t c0 = (uintptr_t)c, c1 = c0 + (uintptr_t)(m * n * esz);
+    if (r0 < c1 && c0 < r1) return set_error(FORGEML_EINVAL, "the residual partly overlaps C");
   }
+  if (res == c && res != nullptr && !(srn == 1 && (srm == n || m == 1)))
+    return set_error(FORGEML_EINVAL, "a residual that is C must have C's strides (N, 1)");
   const TileConfig& t = kTiles[plan.config_id];
   if (plan.ws_need > 0) {
     if (workspace == nullptr || workspace_bytes < plan.ws_need)
@@ -388,6 +400,9 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.k = (int)k;
   p.act = act;
   p.has_bias = bias != nullptr;
+  p.res = (const char*)res;
+  p.srm = srm;
+  p.srn = srn;
   p.tiles_m = (int)cdiv(m, t.bm);
   p.tiles_n = (int)cdiv(n, t.bn);
   p.group_m = p.tiles_m < 8 ? p.tiles_m : 8;
@@ -395,6 +410,26 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int
   p.kslice = plan.split.kslice;
   p.ws = plan.ws_need > 0 ? (float*)workspace : nullptr;
   return t.launch[dtype](p, plan.combo, (hipStream_t)stream);
+}
+
+}  // namespace forgeml
+
+extern "C" {
+
+int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
+                     const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
+                     int32_t act, int32_t config_id, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_impl(a, sam, sak, b, sbk, sbn, bias, sbi, c, nullptr, 0, 0, m, n, k, dtype, act, config_id, workspace,
+                   workspace_bytes, stream);
+}
+
+int forgeml_hip_gemm_add(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
+                         const void* bias, int64_t sbi, const void* r, int64_t srm, int64_t srn, void* c, int64_t m,
+                         int64_t n, int64_t k, int32_t dtype, int32_t act, int32_t config_id, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  if (r == nullptr) return set_error(FORGEML_EINVAL, "gemm_add: the residual must be non-NULL");
+  return gemm_impl(a, sam, sak, b, sbk, sbn, bias, sbi, c, r, srm, srn, m, n, k, dtype, act, config_id, workspace,
+                   workspace_bytes, stream);
 }
 
 }  // extern "C"

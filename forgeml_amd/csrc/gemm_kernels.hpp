@@ -58,6 +58,10 @@ struct GemmArgs {
   int m, n, k;
   int act;
   int has_bias;
+  // Optional residual R[M,N] (element (m,n) at res + m*srm + n*srn elements),
+  // added after the activation: C = rnd(act(...) + R).  res may equal c.
+  const char* res;
+  int64_t srm, srn;
   int tiles_m, tiles_n;
   int group_m;
   // Split K: `splits` workgroups share each output tile, slice z covering
@@ -95,6 +99,12 @@ __device__ __forceinline__ float load_as_f32(const char* p) {
   if constexpr (DT == DT_F32) return *(const float*)p;
   else if constexpr (DT == DT_BF16) return bf16_to_f32(*(const uint16_t*)p);
   else return f16_to_f32(*(const uint16_t*)p);
+}
+
+// Residual value (row, col) as fp32.
+template <int DT>
+__device__ __forceinline__ float residual_at(const GemmArgs& p, int row, int col) {
+  return load_as_f32<DT>(p.res + ((int64_t)row * p.srm + (int64_t)col * p.srn) * DTraits<DT>::ESZ);
 }
 
 // Round a float to the output dtype and back (identity for fp32).  gfx950
@@ -648,6 +658,25 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[
           if (p.has_bias) x = round_to<DT>(x + bias[tn][j]);
           v[j] = activate<DT, ACT>(x);
         }
+        if (p.res != nullptr && (INTERIOR || row < p.m)) {
+          // Residual add after the activation, rounded like torch's add.
+          const char* rp = p.res + ((int64_t)row * p.srm + (int64_t)col * p.srn) * ESZ;
+          if (p.srn == 1 && (((uintptr_t)rp) & 15) == 0 && (INTERIOR || col + EPV <= p.n)) {
+            const u32x4 w = *(const u32x4*)rp;
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) {
+              const uint32_t word = w[j * ESZ / 4];
+              const float r = ESZ == 4 ? __uint_as_float(word)
+                                       : (DT == DT_BF16 ? bf16_to_f32((word >> (16 * (j & 1))) & 0xffffu)
+                                                        : f16_to_f32((word >> (16 * (j & 1))) & 0xffffu));
+              v[j] = round_to<DT>(v[j] + r);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < EPV; ++j)
+              if (INTERIOR || col + j < p.n) v[j] = round_to<DT>(v[j] + residual_at<DT>(p, row, col + j));
+          }
+        }
         if (INTERIOR || row < p.m) {
           char* dst = p.c + ((int64_t)row * p.n + col) * ESZ;
           if (vec_ok && (INTERIOR || col + EPV <= p.n)) {
@@ -814,6 +843,7 @@ void fused_gemm_kernel(GemmArgs p) {
     GemmArgs q = p;
     q.c = (char*)(p.ws + (int64_t)z * p.m * p.n);
     q.has_bias = 0;
+    q.res = nullptr;
     const bool interior_ws = row0 + BM <= p.m && col0 + BN <= p.n && (p.n % 4) == 0 && (((uintptr_t)q.c) & 15) == 0;
     epilogue_dispatch<DT_F32, ACT_NONE, TM, TN>(q, acc, buf, row_base, col_base, lane, interior_ws);
     return;
@@ -839,6 +869,8 @@ struct ReduceArgs {
   const float* ws;
   const char* bias;
   char* c;
+  const char* res;  // optional residual, added after the activation
+  int64_t srm, srn;
   int64_t sbi;
   int64_t mn;  // M * N
   int n, splits, has_bias;
@@ -873,12 +905,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs p) {
       for (int j = 0; j < cnt; ++j) v[j] += p.ws[(int64_t)z * p.mn + e0 + j];
   }
   int col = (int)(e0 % p.n);
+  int64_t row = e0 / p.n;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float x = round_to<DT>(v[j]);
     if (p.has_bias && j < cnt) x = round_to<DT>(x + load_as_f32<DT>(p.bias + (int64_t)col * p.sbi * ESZ));
-    v[j] = activate<DT, ACT>(x);
-    col = col + 1 == p.n ? 0 : col + 1;
+    x = activate<DT, ACT>(x);
+    if (p.res != nullptr && j < cnt) x = round_to<DT>(x + load_as_f32<DT>(p.res + (row * p.srm + (int64_t)col * p.srn) * ESZ));
+    v[j] = x;
+    if (col + 1 == p.n) {
+      col = 0;
+      ++row;
+    } else {
+      ++col;
+    }
   }
   char* dst = p.c + e0 * ESZ;
   if (p.vec) {

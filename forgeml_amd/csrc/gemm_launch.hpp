@@ -39,6 +39,9 @@ int launch_reduce(const GemmArgs& p, hipStream_t stream) {
   r.bias = p.bias;
   r.c = p.c;
   r.sbi = p.sbi;
+  r.res = p.res;
+  r.srm = p.srm;
+  r.srn = p.srn;
   r.mn = (int64_t)p.m * p.n;
   r.n = p.n;
   r.splits = p.splits;

@@ -150,6 +150,7 @@ def launch(
     config_id: int,
     workspace: torch.Tensor | None = None,
     stream: int | None = None,
+    residual: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Unchecked launch of the fused kernel (arguments already validated)."""
     lib = _native.load()
@@ -159,12 +160,18 @@ def launch(
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
-    rc = lib.forgeml_hip_gemm(
-        a.data_ptr(), a.stride(0), a.stride(1),
-        b.data_ptr(), b.stride(0), b.stride(1),
-        None if bias is None else bias.data_ptr(), 0 if bias is None else bias.stride(0),
-        out.data_ptr(), m, n, k, dtype, act, config_id, ws_ptr, ws_bytes, ctypes.c_void_p(stream),
-    )
+    bias_ptr, sbi = (None, 0) if bias is None else (bias.data_ptr(), bias.stride(0))
+    if residual is None:
+        rc = lib.forgeml_hip_gemm(
+            a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1), bias_ptr, sbi,
+            out.data_ptr(), m, n, k, dtype, act, config_id, ws_ptr, ws_bytes, ctypes.c_void_p(stream),
+        )
+    else:
+        rc = lib.forgeml_hip_gemm_add(
+            a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1), bias_ptr, sbi,
+            residual.data_ptr(), residual.stride(0), residual.stride(1),
+            out.data_ptr(), m, n, k, dtype, act, config_id, ws_ptr, ws_bytes, ctypes.c_void_p(stream),
+        )
     if rc != _native.OK:
         msg = f"forgeml_hip_gemm failed ({rc}): {_native.last_error()}"
         raise GraphError(msg) if rc in (_native.EINVAL, _native.ECONFIG) else RuntimeError(msg)
@@ -212,12 +219,16 @@ def matmul(
     approximate: str = "none",
     config: KernelConfig = DEFAULT_CONFIG,
     out: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """out = act(rnd(rnd(a @ b) + bias)) on the gfx950 kernels.
 
     ``activation`` is "none", "gelu" (``approximate`` "none" = erf, "tanh")
     or "relu" (clamp_min(x, 0), the executor's relu slot writer fused into
-    the epilogue).  Launches on ``torch.cuda.current_stream()`` of ``a``'s
+    the epilogue).  ``residual`` (keyword only, not in the reference's
+    signature) adds an [M, N] tensor after the activation in the same
+    epilogue, as the reference's following ``add`` node would; it may be
+    ``out`` itself.  Launches on ``torch.cuda.current_stream()`` of ``a``'s
     device and returns ``out`` (allocated when None).
     """
     if not torch.cuda.is_available():
@@ -250,6 +261,13 @@ def matmul(
         or bias.shape[0] != n
     ):
         raise GraphError("bias must be a 1-D GPU tensor of output width matching dtype/device")
+    if residual is not None and (
+        not isinstance(residual, torch.Tensor)
+        or residual.device != a.device
+        or residual.dtype != a.dtype
+        or tuple(residual.shape) != (m, n)
+    ):
+        raise GraphError("residual must be a GPU tensor of shape (M, N) matching dtype/device")
     cid = _check_config(config, a.dtype)
     if _device_arch(a.device) != TARGET_ARCH:
         raise GraphError(f"the HIP kernels are built for {TARGET_ARCH}; device {a.device} is {_device_arch(a.device)}")
@@ -268,10 +286,17 @@ def matmul(
         for src in (a, b, bias):
             if src is not None and src.untyped_storage().data_ptr() == out_ptr:
                 raise GraphError("out must not share storage with inputs")
+        if (
+            residual is not None
+            and residual.untyped_storage().data_ptr() == out_ptr
+            and (residual.data_ptr() != out.data_ptr() or residual.stride() != out.stride())
+        ):
+            raise GraphError("residual must be out itself or not share its storage")
     with torch.cuda.device(a.device):
         nbytes = plan(a, b, config)["workspace_bytes"]
         ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
-        return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws)
+        return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws,
+                      residual=residual)
 
 
 def select_kernels(graph: Graph, backend: str) -> dict[str, str]:

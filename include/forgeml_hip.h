@@ -89,6 +89,29 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
                      void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/*
+ * Fused GEMM + bias + activation + residual add:
+ *
+ *     C = rnd( act( rnd( rnd(A·B) + bias ) ) + R )
+ *
+ * i.e. forgeml_hip_gemm followed, in the same epilogue, by the `add` node
+ * the reference's executor runs next on the GEMM's result (the residual
+ * connections of the transformer block: ops.py's `add`, compiled by the
+ * torch slot writer at src/forgeml/compiler.py:93-98).  R[M,N] has element
+ * (m,n) at r + (m*srm + n*srn) elements and may be C itself (strides N, 1),
+ * but must not partly overlap it.  Other arguments, errors and workspace
+ * rules are forgeml_hip_gemm's.  No reference counterpart as one call: the
+ * reference runs the GEMM and the add as two kernels.
+ */
+int forgeml_hip_gemm_add(const void* a, int64_t sam, int64_t sak,
+                         const void* b, int64_t sbk, int64_t sbn,
+                         const void* bias, int64_t sbi,
+                         const void* r, int64_t srm, int64_t srn,
+                         void* c, int64_t m, int64_t n, int64_t k,
+                         int32_t dtype, int32_t act, int32_t config_id,
+                         void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
 /* What forgeml_hip_gemm would run for these operands, without launching:
  *   out[0]  the config id (resolved when config_id is FORGEML_CONFIG_AUTO)
  *   out[1]  the number of K slices (1 = K is not split)
@@ -131,7 +154,7 @@ const char* forgeml_hip_last_error(void);
 /* ABI version of this header; bumped on any signature change. */
 int forgeml_hip_abi_version(void);
 
-#define FORGEML_HIP_ABI_VERSION 2
+#define FORGEML_HIP_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

@@ -86,6 +86,8 @@ def test_compiled_transformer_block_matches_cpu_path(gpu):
     plan = compiled.kernel_plan
     gemm_nodes = [n.name for n in compiled.graph.nodes if n.op in kernels.GEMM_OPS]
     assert len(gemm_nodes) == 4 and all(plan[n] == "hip" for n in gemm_nodes)
+    # Both residual adds ride in the out-projection and FFN-down epilogues.
+    assert len(compiled.fused_residuals) == 2
     _say("compiled transformer block")
     torch.backends.cuda.matmul.allow_tf32 = False
     got = compiled(xg).cpu()

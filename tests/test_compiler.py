@@ -130,6 +130,61 @@ def test_gpu_dispatch_path_with_fake_kernel(monkeypatch):
     assert seen == [("gelu", "tanh", True, True), ("none", "none", True, False)]
 
 
+def _fake_matmul_residual(seen):
+    def fake(a, b, bias=None, *, activation="none", approximate="none", config=None, out=None, residual=None):
+        seen.append(residual is not None)
+        value = a @ b + (bias if bias is not None else 0)
+        if activation == "gelu":
+            value = torch.nn.functional.gelu(value, approximate=approximate)
+        if residual is not None:
+            value = value + residual
+        return value if out is None else out.copy_(value)
+    return fake
+
+
+def test_gemm_and_residual_add_fuse_on_hip_plan(monkeypatch):
+    from forgeml_amd.neural import TransformerBlock
+
+    torch.manual_seed(0)
+    block = TransformerBlock(64, 4, 128).eval()
+    x = torch.randn(2, 8, 64)
+    c = forgeml_amd.compile(block, (x,))
+    expected = c(x)
+    assert c.fused_residuals == {}  # torch backend: the reference's two kernels
+    seen = []
+    monkeypatch.setattr(kernels, "matmul", _fake_matmul_residual(seen))
+    c.kernel_plan = {n.name: ("hip" if n.op in kernels.GEMM_OPS else "torch") for n in c.graph.nodes}
+    # out-proj -> reshape -> add(x, .) and FFN down -> reshape -> add(h, .), the
+    # second writing the graph output.
+    assert sorted((g, add) for g, (add, _v, _r, _c) in c.fused_residuals.items()) == [("down", "add_1"), ("o", "add")]
+    torch.testing.assert_close(c(x), expected, rtol=1e-5, atol=1e-5)
+    assert seen.count(True) == 2 and len(seen) == 4
+    # Outputs stay fresh per call; calls are repeatable.
+    first = c(x)
+    second = c(x)
+    assert first.data_ptr() != second.data_ptr()
+    torch.testing.assert_close(first, second, rtol=0, atol=0)
+
+
+def test_residual_fusion_needs_adjacency_and_exclusive_use():
+    b = GraphBuilder({"x": spec(4, 8), "r": spec(4, 16)})
+    w = b.constant("w", torch.randn(8, 16))
+    b.add("y", "linear", ("x", w))
+    b.add("z", "relu", ("r",))  # between the GEMM and its add: no fusion
+    b.add("s", "add", ("y", "z"))
+    c = forgeml_amd.compile(b.finish(("s",)), optimize=False)
+    object.__setattr__(c, "kernel_plan", {"y": "hip", "z": "torch", "s": "torch"})
+    assert c._plan_residual_fusions() == {}
+    b = GraphBuilder({"x": spec(4, 8), "r": spec(4, 16)})
+    w = b.constant("w", torch.randn(8, 16))
+    b.add("y", "linear", ("x", w))
+    b.add("s", "add", ("y", "r"))
+    b.add("t", "add", ("s", "y"))  # y has a second consumer: no fusion
+    c = forgeml_amd.compile(b.finish(("t",)), optimize=False)
+    object.__setattr__(c, "kernel_plan", {"y": "hip", "s": "torch", "t": "torch"})
+    assert c._plan_residual_fusions() == {}
+
+
 def test_hip_plan_stores_weights_k_contiguous(monkeypatch):
     monkeypatch.setattr(kernels, "matmul", _fake_matmul([]))
     model = make_mlp()

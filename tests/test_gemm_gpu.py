@@ -292,6 +292,52 @@ def test_few_row_kernel_strided_rows_and_determinism(gpu):
           "few-row auto")
 
 
+# -- residual add in the epilogue (forgeml_hip_gemm_add) --------------------------
+
+def _with_residual(expected: torch.Tensor, r: torch.Tensor) -> torch.Tensor:
+    # The reference's add node after the GEMM: torch add in the dtype.
+    return expected + r.to(expected.dtype)
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_residual_add_every_kernel(gpu, dtype):
+    # (M, N, K, B layout): a tiled launch, a split-K launch, a few-row launch.
+    cases = [(300, 200, 136, "nt"), (5, 640, 3000, "nn"), (7, 3072, 512, "nt")]
+    for m, n, k, layout in cases:
+        seed = case_seed("residual", m, n, k, dtype)
+        a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout=layout)
+        g = torch.Generator().manual_seed(seed + 1)
+        r = torch.randn(m, n, generator=g).to(dtype)
+        a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+        kind = kernels.plan(a_d, b_d)
+        for activation in ("none", "gelu"):
+            what = f"residual M={m} N={n} K={k} {dtype} {kind['kernel']} splits={kind['k_splits']} act={activation}"
+            _say(what)
+            expected = _with_residual(reference_cpu(a, b, bias, activation), r)
+            got = kernels.matmul(a_d, b_d, bias_d, activation=activation, residual=r.to(gpu))
+            _gate(got, expected, k, what)
+            # In place: the residual is the output buffer itself.
+            out = r.to(gpu)
+            kernels.matmul(a_d, b_d, bias_d, activation=activation, residual=out, out=out)
+            _gate(out, expected, k, what + " in place")
+        # A residual with other strides (a transposed view).
+        rt = r.t().contiguous().to(gpu).t()
+        got = kernels.matmul(a_d, b_d, bias_d, residual=rt)
+        _gate(got, _with_residual(reference_cpu(a, b, bias), r), k, f"residual strided M={m} N={n} {dtype}")
+
+
+def test_residual_argument_checks(gpu):
+    a = torch.randn(8, 16, device=gpu)
+    b = torch.randn(16, 32, device=gpu)
+    with pytest.raises(GraphError, match="residual"):
+        kernels.matmul(a, b, residual=torch.randn(8, 31, device=gpu))
+    with pytest.raises(GraphError, match="residual"):
+        kernels.matmul(a, b, residual=torch.randn(8, 32, device=gpu, dtype=torch.bfloat16))
+    base = torch.empty(16, 32, device=gpu)
+    with pytest.raises(GraphError, match="residual"):
+        kernels.matmul(a, b, out=base[:8], residual=base[4:12])
+
+
 def test_deterministic(gpu):
     a, b, bias = gemm_inputs(512, 768, 1024, torch.bfloat16, seed=case_seed("det"))
     a, b, bias = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
