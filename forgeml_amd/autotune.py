@@ -45,7 +45,7 @@ def tune_graph(
     for node in compiled.graph.nodes:
         args = tuple(values[name] for name in node.inputs)
         expected = evaluate(node.op, args, node.attrs)
-        if compiled.kernel_plan.get(node.name) == "hip":
+        if compiled.kernel_plan.get(node.name) == "hip" and node.op in kernels.GEMM_OPS:
             bias = args[2] if len(args) == 3 else None
             activation = "gelu" if node.op == "fused_linear_gelu" else "none"
             approximate = node.attrs.get("approximate", "none") if activation == "gelu" else "none"

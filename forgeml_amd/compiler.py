@@ -236,6 +236,14 @@ class CompiledModel:
             if is_output:
                 return lambda args: self._evaluate(node, args).clone()
             return lambda args: self._evaluate(node, args)
+        if on_hip and node.op == "layer_norm":
+            attrs = node.attrs
+            return lambda args: kernels.layer_norm(
+                args[0], attrs["normalized_shape"], *(args[1:] if len(args) == 3 else (None, None)), eps=attrs["eps"]
+            )
+        if on_hip and node.op == "sdpa":
+            causal, scale = node.attrs["is_causal"], node.attrs.get("scale")
+            return lambda args: kernels.attention(args[0], args[1], args[2], is_causal=causal, scale=scale)
         if on_hip:
             view = None if is_output else self._views.get(node.name)
             return lambda args: self._run_hip(node, args, view)

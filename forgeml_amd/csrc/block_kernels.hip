@@ -1,0 +1,437 @@
+// block_kernels.hip — the transformer block's non-GEMM hot ops on gfx950:
+// LayerNorm over the last dimension and causal scaled-dot-product attention.
+//
+// ForgeML evaluates both with torch (src/forgeml/ops.py: `layer_norm` ->
+// F.layer_norm, `sdpa` -> F.scaled_dot_product_attention), in the compiled
+// transformer block between the GEMMs (src/forgeml/neural.py:18-53).
+//
+// LayerNorm: one wave per row; the row is held in registers as 16-byte
+// vectors, mean and variance are two passes over those registers with wave
+// reductions in a fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
+// fp32, rounded once to the output dtype.
+//
+// Attention (fp32, head dim D of 32, 64 or 96): flash-style,
+// one wave per 32 query rows, streaming 32-key blocks with an online softmax.
+// The wave computes S^T = K Q^T on v_mfma_f32_32x32x2_f32, so that each lane
+// owns one query column of S^T: the softmax row statistics are a reduction
+// over the lane's 16 accumulator values plus one exchange with the other half
+// wave, and the lane's probabilities are already the B operand of
+// O^T += V^T P^T (the MFMA's K index runs over the keys the lane holds).  The
+// output tile is transposed through LDS and stored as 16-byte rows.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdint>
+
+#include "forgeml_hip.h"
+#include "gemm_kernels.hpp"
+
+namespace forgeml {
+
+int set_error(int code, const char* fmt, ...);
+
+// ---------------------------------------------------------------------------
+// LayerNorm
+
+struct LnArgs {
+  const char* x;
+  const char* w;  // nullable (then b is null too)
+  const char* b;
+  char* y;
+  int64_t sx;  // row stride of x, elements
+  int rows, cols;
+  float eps;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// The 16 / ESZ values of a 16-byte vector, as fp32.
+template <int DT>
+__device__ __forceinline__ void unpack16(const u32x4& w, float (&out)[16 / DTraits<DT>::ESZ]) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+#pragma unroll
+  for (int e = 0; e < 16 / ESZ; ++e) {
+    const uint32_t word = w[e * ESZ / 4];
+    if constexpr (ESZ == 4) out[e] = __uint_as_float(word);
+    else if constexpr (DT == DT_BF16) out[e] = bf16_to_f32((word >> (16 * (e & 1))) & 0xffffu);
+    else out[e] = f16_to_f32((word >> (16 * (e & 1))) & 0xffffu);
+  }
+}
+
+// Row held in registers: VPL 16-byte vectors per lane.
+template <int DT, int VPL>
+__global__ __launch_bounds__(256) void layer_norm_kernel(LnArgs p) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  constexpr int VEC = 16 / ESZ;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;  // whole wave: no barrier below
+  const char* xr = p.x + (int64_t)row * p.sx * ESZ;
+  float v[VPL][VEC];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c0 = (lane + 64 * i) * VEC;
+    if (c0 < p.cols) {
+      unpack16<DT>(*(const u32x4*)(xr + (int64_t)c0 * ESZ), v[i]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += v[i][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[i][e] = 0.0f;
+    }
+  }
+  const float mean = wave_sum(sum) / (float)p.cols;
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c0 = (lane + 64 * i) * VEC;
+    if (c0 < p.cols) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = v[i][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)p.cols + p.eps);
+  char* yr = p.y + (int64_t)row * p.cols * ESZ;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c0 = (lane + 64 * i) * VEC;
+    if (c0 < p.cols) {
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] - mean) * rstd;
+      if (p.w != nullptr) {
+        // Weight and bias as 16-byte vectors, like the row.
+        float wv[VEC], bv[VEC];
+        unpack16<DT>(*(const u32x4*)(p.w + (int64_t)c0 * ESZ), wv);
+        unpack16<DT>(*(const u32x4*)(p.b + (int64_t)c0 * ESZ), bv);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = o[e] * wv[e] + bv[e];
+      }
+      u32x4 w;
+      if constexpr (ESZ == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(o[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack2<DT>(o[2 * e], o[2 * e + 1]);
+      }
+      *(u32x4*)(yr + (int64_t)c0 * ESZ) = w;
+    }
+  }
+}
+
+// Any width or alignment: element loads, the row read three times.
+template <int DT>
+__global__ __launch_bounds__(256) void layer_norm_any_kernel(LnArgs p) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const char* xr = p.x + (int64_t)row * p.sx * ESZ;
+  float sum = 0.0f;
+  for (int c = lane; c < p.cols; c += 64) sum += load_as_f32<DT>(xr + (int64_t)c * ESZ);
+  const float mean = wave_sum(sum) / (float)p.cols;
+  float sq = 0.0f;
+  for (int c = lane; c < p.cols; c += 64) {
+    const float d = load_as_f32<DT>(xr + (int64_t)c * ESZ) - mean;
+    sq += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)p.cols + p.eps);
+  char* yr = p.y + (int64_t)row * p.cols * ESZ;
+  for (int c = lane; c < p.cols; c += 64) {
+    float t = (load_as_f32<DT>(xr + (int64_t)c * ESZ) - mean) * rstd;
+    if (p.w != nullptr) t = t * load_as_f32<DT>(p.w + (int64_t)c * ESZ) + load_as_f32<DT>(p.b + (int64_t)c * ESZ);
+    store_from_f32<DT>(yr + (int64_t)c * ESZ, t);
+  }
+}
+
+template <int DT>
+static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
+  constexpr int VEC = 16 / DTraits<DT>::ESZ;
+  const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
+  const int per_lane = (p.cols + 64 * VEC - 1) / (64 * VEC);
+  if (!vec || per_lane > 8) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
+  else if (per_lane <= 1) hipLaunchKernelGGL((layer_norm_kernel<DT, 1>), grid, block, 0, stream, p);
+  else if (per_lane <= 2) hipLaunchKernelGGL((layer_norm_kernel<DT, 2>), grid, block, 0, stream, p);
+  else if (per_lane <= 4) hipLaunchKernelGGL((layer_norm_kernel<DT, 4>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((layer_norm_kernel<DT, 8>), grid, block, 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FORGEML_EHIP, "layer_norm launch failed: %s", hipGetErrorString(e));
+  return FORGEML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Causal (or full) attention, fp32.
+
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t sq[4], sk[4], sv[4], so[4];  // element strides (batch, head, sequence, dim)
+  int batch, heads, lq, lk;
+  int nqb;       // query blocks of 32 per (batch, head)
+  int nitems;    // work items per (batch, head): query blocks, or causal pairs of them
+  int causal;
+  float scale_log2;  // scale * log2(e): softmax in base 2
+};
+
+constexpr int kAttnWaves = 4;
+
+// One wave: one work item of head (b, h).  A work item is query block qb
+// (rows [32*qb, 32*qb + 32)); with the causal mask it is the pair of blocks t
+// and nqb-1-t, whose key blocks add up to nqb+1 for every t, so all waves
+// carry the same work and none waits on the longest rows alone.
+template <int D>
+__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) {
+  static_assert(D % 32 == 0 && D <= 96, "head dim must be 32, 64 or 96");
+  constexpr int NC = D / 8;   // 8-element chunks of the head dim
+  constexpr int NB = D / 32;  // 32-row blocks of O^T
+  __shared__ float tr[kAttnWaves][32][D + 1];  // output transpose; odd row length: conflict-free column writes
+
+  const int lane = threadIdx.x & 63, half = lane >> 5, lc = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x * kAttnWaves + wave;
+  const int nbh = p.batch * p.heads;
+  if (g >= nbh * p.nitems) return;  // whole wave; no workgroup barrier below
+  const int t = g / nbh, bh = g % nbh;
+  const int b = bh / p.heads, h = bh % p.heads;
+  const int nrep = (p.causal && t != p.nqb - 1 - t) ? 2 : 1;
+  const float* qp = p.q + b * p.sq[0] + h * p.sq[1];
+  const float* kp = p.k + b * p.sk[0] + h * p.sk[1];
+  const float* vp = p.v + b * p.sv[0] + h * p.sv[1];
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc((const char*)qp, (uint32_t)(((int64_t)(p.lq - 1) * p.sq[2] + D) * 4));
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc((const char*)kp, (uint32_t)(((int64_t)(p.lk - 1) * p.sk[2] + D) * 4));
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc((const char*)vp, (uint32_t)(((int64_t)(p.lk - 1) * p.sv[2] + D) * 4));
+
+  for (int rep = 0; rep < nrep; ++rep) {
+  const int qb = rep == 0 ? (p.causal ? p.nqb - 1 - t : t) : t;
+  const int q0 = qb * 32;
+  // Q^T operand: this lane's query row lc, dims 8c + 4*half + e.
+  const int qrow = q0 + lc;
+  u32x4 qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t off = qrow < p.lq ? (uint32_t)(((int64_t)qrow * p.sq[2] + 8 * c + 4 * half) * 4) : kOutOfRange;
+    qf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, (int)off, 0, 0));
+  }
+
+  const int last_key = p.causal ? min(p.lk, q0 + 32) : p.lk;  // keys [0, last_key) can be visible
+  const int nkb = (last_key + 31) / 32;
+
+  auto load_k = [&](int kb, u32x4 (&kf)[NC]) {
+    const int key = kb * 32 + lc;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t off =
+          (kb < nkb && key < p.lk) ? (uint32_t)(((int64_t)key * p.sk[2] + 8 * c + 4 * half) * 4) : kOutOfRange;
+      kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)off, 0, 0));
+    }
+  };
+
+  f32x16 o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[nb][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  u32x4 kf[NC], kn[NC];
+  load_k(0, kf);
+  for (int kb = 0; kb < nkb; ++kb) {
+    // V^T operand for this block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
+    float vf[NB][16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int key = kb * 32 + 8 * (s >> 2) + 4 * half + (s & 3);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t off = key < p.lk ? (uint32_t)(((int64_t)key * p.sv[2] + lc + 32 * nb) * 4) : kOutOfRange;
+        vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)off, 0, 0));
+      }
+    }
+    load_k(kb + 1, kn);
+
+    // S^T[key][query] for this block.
+    f32x16 s = {};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c][e]), __uint_as_float(qf[c][e]), s, 0, 0, 0);
+
+    // Online softmax for query qrow (this lane's column), keys of this half.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+      const bool ok = key < p.lk && (!p.causal || key <= qrow);
+      s[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
+      mx = fmaxf(mx, s[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float base = m_new == -INFINITY ? 0.0f : m_new;  // rows with nothing visible yet
+    const float alpha = exp2f(m - base);
+    float rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] = exp2f(s[i] - base);
+      rs += s[i];
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+    m = m_new;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[nb][i] *= alpha;
+
+    // O^T[dim][query] += V^T[dim][key] P^T[key][query]: step i takes the key of
+    // this lane's accumulator value i.
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[nb][i], s[i], o[nb], 0, 0, 0);
+
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kf[c] = kn[c];
+  }
+
+  // Normalise, transpose through LDS (this wave's slice only), store rows.
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tr[wave][lc][nb * 32 + 8 * (i >> 2) + 4 * half + (i & 3)] = o[nb][i] * inv;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float* op = p.o + b * p.so[0] + h * p.so[1];
+  constexpr int VPR = D / 4;  // 16-byte vectors per output row
+  for (int idx = lane; idx < 32 * VPR; idx += 64) {
+    const int r = idx / VPR, c4 = (idx % VPR) * 4;
+    const int qi = q0 + r;
+    if (qi < p.lq) {
+      float* dst = op + (int64_t)qi * p.so[2] + c4;
+      const float4 val = make_float4(tr[wave][r][c4], tr[wave][r][c4 + 1], tr[wave][r][c4 + 2], tr[wave][r][c4 + 3]);
+      if (p.so[3] == 1 && (((uintptr_t)dst) & 15) == 0) {
+        *(float4*)dst = val;
+      } else {
+        dst[0] = val.x;
+        dst[p.so[3]] = val.y;
+        dst[2 * p.so[3]] = val.z;
+        dst[3 * p.so[3]] = val.w;
+      }
+    }
+  }
+  // This wave's next item reuses the transpose buffer after these reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+template <int D>
+static int launch_attention(const AttnArgs& p, hipStream_t stream) {
+  const int64_t waves = (int64_t)p.batch * p.heads * p.nitems;
+  hipLaunchKernelGGL((attention_kernel<D>), dim3((unsigned)((waves + kAttnWaves - 1) / kAttnWaves)),
+                     dim3(kAttnWaves * 64), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FORGEML_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+  return FORGEML_OK;
+}
+
+}  // namespace forgeml
+
+using namespace forgeml;
+
+extern "C" {
+
+int forgeml_hip_layer_norm(const void* x, int64_t sx, const void* w, const void* b, void* y, int64_t rows,
+                           int64_t cols, float eps, int32_t dtype, void* stream) {
+  if (x == nullptr || y == nullptr) return set_error(FORGEML_EINVAL, "layer_norm: x and y must be non-NULL");
+  if ((w == nullptr) != (b == nullptr)) return set_error(FORGEML_EINVAL, "layer_norm: give both weight and bias or neither");
+  if (rows <= 0 || cols <= 0 || rows > INT_MAX || cols > INT_MAX || sx < cols)
+    return set_error(FORGEML_EINVAL, "layer_norm: bad shape or row stride");
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return set_error(FORGEML_EINVAL, "layer_norm: eps must be finite and positive");
+  if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
+  const int esz = dtype == FORGEML_DTYPE_F32 ? 4 : 2;
+  LnArgs p;
+  p.x = (const char*)x;
+  p.w = (const char*)w;
+  p.b = (const char*)b;
+  p.y = (char*)y;
+  p.sx = sx;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.eps = eps;
+  const bool vec = (cols * esz) % 16 == 0 && (sx * esz) % 16 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+                   ((uintptr_t)w & 15) == 0 && ((uintptr_t)b & 15) == 0;
+  switch (dtype) {
+    case FORGEML_DTYPE_F32: return launch_layer_norm<DT_F32>(p, vec, (hipStream_t)stream);
+    case FORGEML_DTYPE_BF16: return launch_layer_norm<DT_BF16>(p, vec, (hipStream_t)stream);
+    default: return launch_layer_norm<DT_F16>(p, vec, (hipStream_t)stream);
+  }
+}
+
+int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                          const int64_t* sv, void* o, const int64_t* so, int64_t batch, int64_t heads, int64_t lq,
+                          int64_t lk, int64_t dim, int32_t causal, float scale, int32_t dtype, void* stream) {
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || sq == nullptr || sk == nullptr || sv == nullptr ||
+      so == nullptr)
+    return set_error(FORGEML_EINVAL, "attention: pointers must be non-NULL");
+  if (dtype != FORGEML_DTYPE_F32) return set_error(FORGEML_EINVAL, "attention: only fp32 is built");
+  if (dim != 32 && dim != 64 && dim != 96)
+    return set_error(FORGEML_EINVAL, "attention: head dim must be 32, 64 or 96 (got %lld)", (long long)dim);
+  if (batch <= 0 || heads <= 0 || lq <= 0 || lk <= 0) return set_error(FORGEML_EINVAL, "attention: empty shape");
+  if (sq[3] != 1 || sk[3] != 1 || sv[3] != 1)
+    return set_error(FORGEML_EINVAL, "attention: q, k and v need a unit stride along the head dim");
+  for (int i = 0; i < 4; ++i)
+    if (sq[i] < 0 || sk[i] < 0 || sv[i] < 0 || so[i] < 0) return set_error(FORGEML_EINVAL, "attention: negative stride");
+  if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || (sq[2] % 4) || (sk[2] % 4) || (sq[0] % 4) || (sq[1] % 4) ||
+      (sk[0] % 4) || (sk[1] % 4))
+    return set_error(FORGEML_EINVAL, "attention: q and k rows must be 16-byte aligned");
+  // 32-bit byte offsets within one (batch, head) slice.
+  if (((lq - 1) * sq[2] + dim) * 4 >= ((int64_t)1 << 31) || ((lk - 1) * sk[2] + dim) * 4 >= ((int64_t)1 << 31) ||
+      ((lk - 1) * sv[2] + dim) * 4 >= ((int64_t)1 << 31))
+    return set_error(FORGEML_EINVAL, "attention: a (batch, head) slice exceeds 2 GiB");
+  const int64_t nqb = (lq + 31) / 32;
+  if (batch * heads * nqb > INT_MAX / kAttnWaves) return set_error(FORGEML_EINVAL, "attention: too many query blocks");
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(FORGEML_EINVAL, "attention: scale must be finite and positive");
+  AttnArgs p;
+  p.q = (const float*)q;
+  p.k = (const float*)k;
+  p.v = (const float*)v;
+  p.o = (float*)o;
+  for (int i = 0; i < 4; ++i) {
+    p.sq[i] = sq[i];
+    p.sk[i] = sk[i];
+    p.sv[i] = sv[i];
+    p.so[i] = so[i];
+  }
+  p.batch = (int)batch;
+  p.heads = (int)heads;
+  p.lq = (int)lq;
+  p.lk = (int)lk;
+  p.nqb = (int)nqb;
+  p.nitems = causal ? (int)((nqb + 1) / 2) : (int)nqb;
+  p.causal = causal != 0;
+  p.scale_log2 = scale * 1.44269504088896340736f;
+  switch (dim) {
+    case 32: return launch_attention<32>(p, (hipStream_t)stream);
+    case 64: return launch_attention<64>(p, (hipStream_t)stream);
+    default: return launch_attention<96>(p, (hipStream_t)stream);
+  }
+}
+
+}  // extern "C"

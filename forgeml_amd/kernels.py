@@ -299,8 +299,89 @@ def matmul(
                       residual=residual)
 
 
+# -- the transformer block's other hot ops ----------------------------------------
+
+BLOCK_OPS = ("layer_norm", "sdpa")
+_ATTENTION_DIMS = (32, 64, 96)
+
+
+def _block_op_supported(node, specs) -> bool:
+    """Whether the HIP kernel runs this layer_norm / sdpa node's specs."""
+    if node.op == "layer_norm":
+        return node.spec.dtype in _DTYPES
+    if node.op == "sdpa":
+        q, k = specs[node.inputs[0]], specs[node.inputs[1]]
+        return (len(node.inputs) == 3 and q.dtype == torch.float32 and q.shape[-1] in _ATTENTION_DIMS
+                and k.shape[-1] == q.shape[-1])
+    return False
+
+
+def layer_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = None,
+               bias: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """F.layer_norm over the trailing ``normalized_shape`` dims on the gfx950 kernel."""
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+    normalized_shape = tuple(normalized_shape)
+    if not x.is_cuda or x.dtype not in _DTYPES:
+        raise GraphError("hip layer_norm needs a GPU tensor of fp32, bf16 or fp16")
+    if tuple(x.shape[-len(normalized_shape):]) != normalized_shape:
+        raise GraphError(f"layer_norm shape {tuple(x.shape)} does not end with {normalized_shape}")
+    if (weight is None) != (bias is None):
+        raise GraphError("hip layer_norm takes both weight and bias or neither")
+    cols = 1
+    for d in normalized_shape:
+        cols *= d
+    xc = x.contiguous()
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    w = None if weight is None else weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    rows = xc.numel() // cols
+    rc = _native.load().forgeml_hip_layer_norm(
+        xc.data_ptr(), cols, None if w is None else w.data_ptr(), None if b is None else b.data_ptr(), y.data_ptr(),
+        rows, cols, float(eps), _DTYPE_CODES[x.dtype], ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream),
+    )
+    if rc != _native.OK:
+        raise RuntimeError(f"forgeml_hip_layer_norm failed ({rc}): {_native.last_error()}")
+    return y
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, is_causal: bool = False,
+              scale: float | None = None) -> torch.Tensor:
+    """F.scaled_dot_product_attention (no mask, no dropout) on the gfx950 kernel, fp32.
+
+    The result has shape [B, H, Lq, D] and is stored [B, Lq, H, D] (returned as
+    its transposed view), the layout the block's following transpose + reshape
+    reads without a copy.
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise GraphError("hip attention needs rank-4 GPU tensors [batch, heads, sequence, dim]")
+    if not (q.dtype == k.dtype == v.dtype == torch.float32):
+        raise GraphError("hip attention is built for fp32")
+    bsz, heads, lq, dim = q.shape
+    lk = k.shape[2]
+    if k.shape != (bsz, heads, lk, dim) or v.shape != k.shape or dim not in _ATTENTION_DIMS:
+        raise GraphError(f"hip attention shapes {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)} not supported")
+    qkv = []
+    for t in (q, k, v):
+        if t.stride(3) != 1 or t.data_ptr() % 16 or any(s % 4 for s in t.stride()[:3]):
+            t = t.contiguous()
+        qkv.append(t)
+    out = torch.empty(bsz, lq, heads, dim, dtype=q.dtype, device=q.device).transpose(1, 2)
+    strides = [(ctypes.c_int64 * 4)(*t.stride()) for t in (*qkv, out)]
+    sc = float(scale) if scale is not None else dim ** -0.5
+    rc = _native.load().forgeml_hip_attention(
+        qkv[0].data_ptr(), strides[0], qkv[1].data_ptr(), strides[1], qkv[2].data_ptr(), strides[2],
+        out.data_ptr(), strides[3], bsz, heads, lq, lk, dim, int(bool(is_causal)), sc, _native.DTYPE_F32,
+        ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream),
+    )
+    if rc != _native.OK:
+        raise RuntimeError(f"forgeml_hip_attention failed ({rc}): {_native.last_error()}")
+    return out
+
+
 def select_kernels(graph: Graph, backend: str) -> dict[str, str]:
-    """Per-node backend plan: "hip" for GEMM nodes on a gfx950 GPU, else "torch"."""
+    """Per-node backend plan: "hip" for GEMM nodes on a gfx950 GPU, and for the
+    transformer block's layer_norm / sdpa nodes the HIP kernels support; else "torch"."""
     if backend == "torch":
         return {n.name: "torch" for n in graph.nodes}
     if backend not in ("auto", "hip"):
@@ -316,6 +397,8 @@ def select_kernels(graph: Graph, backend: str) -> dict[str, str]:
     for node in graph.nodes:
         on_gpu = all(torch.device(specs[i].device).type == "cuda" for i in node.inputs)
         if can and node.op in GEMM_OPS and node.spec.dtype in _DTYPES and (backend == "hip" or on_gpu):
+            plan[node.name] = "hip"
+        elif can and on_gpu and node.op in BLOCK_OPS and _block_op_supported(node, specs):
             plan[node.name] = "hip"
         else:
             plan[node.name] = "torch"

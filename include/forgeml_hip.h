@@ -147,6 +147,33 @@ int forgeml_hip_num_configs(void);
  * Counterpart of the KernelConfig fields (src/forgeml/kernels.py:12-18). */
 int forgeml_hip_config_info(int32_t id, int32_t* out);
 
+/*
+ * LayerNorm over the last dimension:
+ *     y[r, :] = (x[r, :] - mean) / sqrt(var + eps) * w + b     (biased variance)
+ * computed in fp32 and rounded once to the dtype.  x has `rows` rows of
+ * `cols` contiguous elements, row stride sx >= cols; y is contiguous.  w and b
+ * ([cols], contiguous) are both given or both NULL.  Replaces the torch call
+ * F.layer_norm of the `layer_norm` op (src/forgeml/ops.py, _layer_norm).
+ */
+int forgeml_hip_layer_norm(const void* x, int64_t sx, const void* w, const void* b,
+                           void* y, int64_t rows, int64_t cols, float eps,
+                           int32_t dtype, void* stream);
+
+/*
+ * Scaled dot-product attention, fp32:
+ *     O = softmax(Q K^T * scale + causal mask) V
+ * per (batch, head), Q [lq, dim], K and V [lk, dim], the causal mask letting
+ * query i see keys j <= i (top-left aligned, as torch's is_causal).  Each of
+ * q, k, v, o is described by 4 element strides (batch, head, sequence, dim);
+ * q, k and v need unit stride along dim and 16-byte aligned rows of q and k.
+ * dim is 32, 64 or 96.  Replaces F.scaled_dot_product_attention of the
+ * `sdpa` op without an attention mask (src/forgeml/ops.py, _sdpa).
+ */
+int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk,
+                          const void* v, const int64_t* sv, void* o, const int64_t* so,
+                          int64_t batch, int64_t heads, int64_t lq, int64_t lk, int64_t dim,
+                          int32_t causal, float scale, int32_t dtype, void* stream);
+
 /* Thread-local text of the last error on this thread ("" if none).
  * The reference raises Python exceptions instead (kernels.py:62-112). */
 const char* forgeml_hip_last_error(void);
@@ -154,7 +181,7 @@ const char* forgeml_hip_last_error(void);
 /* ABI version of this header; bumped on any signature change. */
 int forgeml_hip_abi_version(void);
 
-#define FORGEML_HIP_ABI_VERSION 3
+#define FORGEML_HIP_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

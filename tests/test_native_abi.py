@@ -172,3 +172,22 @@ def test_gemm_plan_reports_what_runs():
     rc, _ = plan(8, 64, 64, 64, 1, -1, 1)  # negative stride
     assert rc == _native.EINVAL
     assert lib.forgeml_hip_gemm_plan(dummy, 4, 1, dummy, 1, 4, 4, 4, 4, f32, -1, None) == _native.EINVAL
+
+
+def test_block_kernel_argument_errors():
+    lib = _native.load()
+    dummy = ctypes.c_void_p(256)
+    f32 = _native.DTYPE_F32
+    assert lib.forgeml_hip_layer_norm(None, 8, None, None, dummy, 4, 8, 1e-5, f32, None) == _native.EINVAL
+    assert lib.forgeml_hip_layer_norm(dummy, 8, dummy, None, dummy, 4, 8, 1e-5, f32, None) == _native.EINVAL
+    assert lib.forgeml_hip_layer_norm(dummy, 4, None, None, dummy, 4, 8, 1e-5, f32, None) == _native.EINVAL  # stride < cols
+    assert lib.forgeml_hip_layer_norm(dummy, 8, None, None, dummy, 4, 8, 0.0, f32, None) == _native.EINVAL
+    st = (ctypes.c_int64 * 4)(4096, 64 * 64, 64, 1)
+    args = (dummy, st, dummy, st, dummy, st, dummy, st)
+    # head dim 48 is not built; fp16 is not built; a non-unit dim stride is refused
+    assert lib.forgeml_hip_attention(*args, 1, 1, 64, 64, 48, 1, 0.125, f32, None) == _native.EINVAL
+    assert "head dim" in _native.last_error()
+    assert lib.forgeml_hip_attention(*args, 1, 1, 64, 64, 64, 1, 0.125, _native.DTYPE_F16, None) == _native.EINVAL
+    bad = (ctypes.c_int64 * 4)(4096, 64 * 64, 64, 2)
+    assert lib.forgeml_hip_attention(dummy, bad, dummy, st, dummy, st, dummy, st, 1, 1, 64, 64, 64, 1, 0.125, f32,
+                                     None) == _native.EINVAL
