@@ -245,38 +245,55 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) 
     for (int i = 0; i < 16; ++i) o[nb][i] = 0.0f;
   float m = -INFINITY, l = 0.0f;
 
-  u32x4 kf[NC], kn[NC];
-  load_k(0, kf);
-  for (int kb = 0; kb < nkb; ++kb) {
-    // V^T operand for this block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
-    float vf[NB][16];
+  // V^T operand of a key block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
+  auto load_v = [&](int kb, float (&vf)[NB][16]) {
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const int key = kb * 32 + 8 * (s >> 2) + 4 * half + (s & 3);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const uint32_t off = key < p.lk ? (uint32_t)(((int64_t)key * p.sv[2] + lc + 32 * nb) * 4) : kOutOfRange;
+        const uint32_t off =
+            (kb < nkb && key < p.lk) ? (uint32_t)(((int64_t)key * p.sv[2] + lc + 32 * nb) * 4) : kOutOfRange;
         vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)off, 0, 0));
       }
     }
+  };
+
+  // K of the next key block loads while this one computes; V loads at the
+  // start of its block and is needed only after S and the softmax.  (Holding
+  // the next block's V too costs more in register moves than it saves.)
+  u32x4 kf[NC], kn[NC];
+  load_k(0, kf);
+  for (int kb = 0; kb < nkb; ++kb) {
+    float vf[NB][16];
+    load_v(kb, vf);
     load_k(kb + 1, kn);
 
-    // S^T[key][query] for this block.
-    f32x16 s = {};
+    // S^T[key][query] for this block, as two independent MFMA chains (even
+    // and odd dim chunks) so consecutive MFMAs do not wait on each other.
+    f32x16 s = {}, s1 = {};
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+    for (int c = 0; c < NC; c += 2)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int e = 0; e < 4; ++e) {
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c][e]), __uint_as_float(qf[c][e]), s, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c + 1][e]), __uint_as_float(qf[c + 1][e]), s1, 0,
+                                                  0, 0);
+      }
 
     // Online softmax for query qrow (this lane's column), keys of this half.
+    // Key blocks entirely visible to every query of the block skip the mask.
     float mx = -INFINITY;
+    const bool full = kb * 32 + 32 <= p.lk && (!p.causal || kb * 32 + 31 <= q0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = kb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-      const bool ok = key < p.lk && (!p.causal || key <= qrow);
-      s[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
-      mx = fmaxf(mx, s[i]);
+      float x = (s[i] + s1[i]) * p.scale_log2;
+      if (!full) {
+        const int key = kb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+        x = (key < p.lk && (!p.causal || key <= qrow)) ? x : -INFINITY;
+      }
+      s[i] = x;
+      mx = fmaxf(mx, x);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m, mx);
