@@ -18,9 +18,9 @@
 
 namespace forgeml {
 
-#define FORGEML_EXTERN_F32(bm, bn, wm, wn) \
+#define FORGEML_EXTERN_F32(bm, bn, wm, wn, ...) \
   extern template int launch_tile<DT_F32, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
-#define FORGEML_EXTERN_H16(bm, bn, wm, wn)                                                      \
+#define FORGEML_EXTERN_H16(bm, bn, wm, wn, ...)                                                 \
   extern template int launch_tile<DT_BF16, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t); \
   extern template int launch_tile<DT_F16, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
 FORGEML_F32_TILES(FORGEML_EXTERN_F32)
@@ -42,16 +42,18 @@ int set_error(int code, const char* fmt, ...) {
 }
 
 static const TileConfig kTiles[] = {
-#define FORGEML_ROW_F32(bm, bn, wm, wn) \
-  {0, bm, bn, wm, wn, KIND_TILED, {&launch_tile<DT_F32, bm, bn, wm, wn>, nullptr, nullptr}},
-#define FORGEML_ROW_H16(bm, bn, wm, wn) \
-  {1, bm, bn, wm, wn, KIND_TILED, {nullptr, &launch_tile<DT_BF16, bm, bn, wm, wn>, &launch_tile<DT_F16, bm, bn, wm, wn>}},
+#define FORGEML_ROW_F32(bm, bn, wm, wn, occ, eff, solo) \
+  {0, bm, bn, wm, wn, KIND_TILED, {&launch_tile<DT_F32, bm, bn, wm, wn>, nullptr, nullptr}, occ, eff, solo},
+#define FORGEML_ROW_H16(bm, bn, wm, wn, occ, eff, solo)                                                            \
+  {1, bm, bn, wm, wn, KIND_TILED, {nullptr, &launch_tile<DT_BF16, bm, bn, wm, wn>, &launch_tile<DT_F16, bm, bn, wm, wn>}, \
+   occ, eff, solo},
     FORGEML_F32_TILES(FORGEML_ROW_F32) FORGEML_H16_TILES(FORGEML_ROW_H16)
 #undef FORGEML_ROW_F32
 #undef FORGEML_ROW_H16
     // Few-row kernels (M <= 64, K-contiguous operands), last so the tiled ids stay put.
-    {0, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {&launch_skinny<DT_F32>, nullptr, nullptr}},
-    {1, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {nullptr, &launch_skinny<DT_BF16>, &launch_skinny<DT_F16>}},
+    {0, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {&launch_skinny<DT_F32>, nullptr, nullptr}, 1, 100, 100},
+    {1, kSkinnyMaxRows, 16, 1, kSkinnyWaves, KIND_SKINNY, {nullptr, &launch_skinny<DT_BF16>, &launch_skinny<DT_F16>}, 1, 100,
+     100},
 };
 static constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -141,44 +143,6 @@ static int skinny_id(int dclass) {
   return -1;
 }
 
-// Shape heuristic behind FORGEML_CONFIG_AUTO: the largest tile that still
-// gives every one of the 256 CUs at least one workgroup (the smallest tile
-// otherwise; split K then adds workgroups).  Among equal areas, more waves
-// per workgroup win (two waves per SIMD hide each other's stalls), but only
-// where both operands are K-contiguous: the 8-wave tile's register budget
-// does not fit the transposing loaders.  Layouts whose kernels exist only for
-// small tiles choose among those, and 16-bit element loads (whose staged
-// values and addresses outgrow the registers of larger tiles) use 64x64.
-static int select_config(int64_t m, int64_t n, int64_t /*k*/, int dtype, int ma, int mb) {
-  const int dclass = dclass_of(dtype);
-  const bool all_k = ma == MODE_K && mb == MODE_K;
-  const int64_t max_area = (dclass == 1 && (ma == MODE_G || mb == MODE_G)) ? 64 * 64
-                           : needs_small_tile(ma, mb)                     ? kSmallTileArea
-                                                                          : INT64_MAX;
-  int best = -1, smallest = -1;
-  int64_t best_area = -1, smallest_area = INT64_MAX;
-  int best_waves = 0;
-  for (int id = 0; id < kNumTiles; ++id) {
-    const TileConfig& t = kTiles[id];
-    if (t.dclass != dclass || t.kind != KIND_TILED) continue;
-    const int waves = t.wm * t.wn;
-    if (waves > 4 && dclass == 1 && !all_k) continue;
-    const int64_t area = (int64_t)t.bm * t.bn;
-    if (area > max_area) continue;
-    if (area < smallest_area) {
-      smallest_area = area;
-      smallest = id;
-    }
-    const int64_t tiles = cdiv(m, t.bm) * cdiv(n, t.bn);
-    if (tiles >= 256 && (area > best_area || (area == best_area && waves > best_waves))) {
-      best_area = area;
-      best_waves = waves;
-      best = id;
-    }
-  }
-  return best >= 0 ? best : smallest;
-}
-
 // K split for a grid of few output tiles: enough workgroups for two per CU,
 // slices of at least kMinSliceStages stages, at most kMaxSplit slices.
 static constexpr int64_t kSplitBelowTiles = 128;
@@ -209,6 +173,61 @@ static SplitPlan split_plan(const TileConfig& t, int64_t m, int64_t n, int64_t k
 static int64_t workspace_bytes_for(const SplitPlan& plan, int64_t m, int64_t n) {
   return plan.splits > 1 ? (int64_t)plan.splits * m * n * (int64_t)sizeof(float) : 0;
 }
+
+// Relative time of a tiled launch, for the shape heuristic.  Workgroups
+// (tiles x K slices) are dealt to the 256 CUs; the busiest CU's share times
+// one workgroup's work (its area times its K slice plus a fixed 8 stages of
+// prologue and epilogue), divided by the tile's efficiency (the solo value
+// when that CU holds fewer workgroups than the tile's occupancy), plus the
+// split planes' traffic.  Fitted to measured times of every tile on MI355X;
+// it picks the fastest tile or one within a few per cent of it.
+static constexpr int64_t kCUs = 256;
+static constexpr int64_t kOverheadStages = 8;
+
+static double tile_cost(const TileConfig& t, int64_t m, int64_t n, int64_t k, int esz) {
+  const SplitPlan sp = split_plan(t, m, n, k, esz);
+  const int64_t bk = kRowBytes / esz;
+  const int64_t units = cdiv(m, t.bm) * cdiv(n, t.bn) * sp.splits;
+  const int64_t per_cu = cdiv(units, kCUs);
+  const double eff = (per_cu >= t.occ ? t.eff : t.solo_eff) / 100.0;
+  const int64_t kwork = std::min(k, (int64_t)sp.kslice * bk) + kOverheadStages * bk;
+  double cost = (double)per_cu * t.bm * t.bn * kwork / eff;
+  if (sp.splits > 1) cost += 2.0 * sp.splits * (double)m * n * 4 * 8 / kCUs;
+  return cost;
+}
+
+// Shape heuristic behind FORGEML_CONFIG_AUTO for the tiled kernels: the
+// lowest tile_cost, larger tiles winning within 1 %.  The 8-wave 16-bit tile
+// is offered only when both operands are K-contiguous (its register budget
+// does not fit the transposing loaders); layouts whose kernels exist only
+// for small tiles choose among those, and 16-bit element loads (whose staged
+// values and addresses outgrow the registers of larger tiles) use 64x64.
+static int select_config(int64_t m, int64_t n, int64_t k, int dtype, int ma, int mb) {
+  const int dclass = dclass_of(dtype);
+  const int esz = esize_of(dtype);
+  const bool all_k = ma == MODE_K && mb == MODE_K;
+  const int64_t max_area = (dclass == 1 && (ma == MODE_G || mb == MODE_G)) ? 64 * 64
+                           : needs_small_tile(ma, mb)                     ? kSmallTileArea
+                                                                          : INT64_MAX;
+  int best = -1;
+  double best_cost = 0.0;
+  for (int id = 0; id < kNumTiles; ++id) {
+    const TileConfig& t = kTiles[id];
+    if (t.dclass != dclass || t.kind != KIND_TILED) continue;
+    if (t.wm * t.wn > 4 && dclass == 1 && !all_k) continue;
+    const int64_t area = (int64_t)t.bm * t.bn;
+    if (area > max_area) continue;
+    const double cost = tile_cost(t, m, n, k, esz);
+    bool take = best < 0 || cost < best_cost * 0.99;  // clearly cheaper
+    if (!take && cost <= best_cost * 1.01) take = area > (int64_t)kTiles[best].bm * kTiles[best].bn;  // a tie: bigger
+    if (take) {
+      best = id;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 
 }  // namespace forgeml
 

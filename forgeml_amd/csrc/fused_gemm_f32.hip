@@ -4,7 +4,7 @@
 #include "tile_table.hpp"
 
 namespace forgeml {
-#define FORGEML_INSTANTIATE(bm, bn, wm, wn) \
+#define FORGEML_INSTANTIATE(bm, bn, wm, wn, ...) \
   template int launch_tile<DT_F32, bm, bn, wm, wn>(const GemmArgs&, int, hipStream_t);
 FORGEML_F32_TILES(FORGEML_INSTANTIATE)
 #undef FORGEML_INSTANTIATE

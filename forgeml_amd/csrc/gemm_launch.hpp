@@ -144,6 +144,7 @@ struct TileConfig {
   int bm, bn, wm, wn;
   int kind;    // KIND_TILED, or KIND_SKINNY (bm = most rows, bn = columns per workgroup)
   TileLauncher launch[3];  // indexed by DT_*; null where not built
+  int occ, eff, solo_eff;  // shape-heuristic constants (see tile_table.hpp)
 };
 
 }  // namespace forgeml
