@@ -233,15 +233,17 @@ struct LoaderK {
       voff[i] = (r < valid_rows && blk < BLOCKS) ? (uint32_t)(r * ld_bytes + c * 16) : kOutOfRange;
     }
   }
-  // Stage kt's K offset goes in the scalar offset; lanes past the K tail get
-  // an out-of-range vector offset.
-  __device__ __forceinline__ void issue(int kt, char* stage) {
+  // DMAs [P0, P1) of this wave's PER for stage kt.  Stage kt's K offset goes
+  // in the scalar offset; lanes past the K tail get an out-of-range vector
+  // offset.
+  template <int P0, int P1>
+  __device__ __forceinline__ void issue_part(int kt, char* stage) {
     // The wave index is uniform: keep the LDS destination (M0) in SGPRs.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kbase = kt * kRowBytes;
     const int klimit = kbytes - kbase;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
+    for (int i = P0; i < P1; ++i) {
       const int blk = wave + i * NWAVES;  // uniform per wave
       if (BLOCKS % NWAVES == 0 || blk < BLOCKS) {
         const uint32_t off = kchunk[i] < klimit ? voff[i] : kOutOfRange;
@@ -249,6 +251,7 @@ struct LoaderK {
       }
     }
   }
+  __device__ __forceinline__ void issue(int kt, char* stage) { issue_part<0, PER>(kt, stage); }
   __device__ __forceinline__ void commit(char*) {}
 };
 
@@ -773,34 +776,50 @@ void fused_gemm_kernel(GemmArgs p) {
   static_assert(S == 2 || (LA::kDirect && LB::kDirect && LA::kExactPer && LB::kExactPer),
                 "rings deeper than two stages count DMA instructions per wave exactly");
 
+  // Two-stage rings of K-contiguous operands split each stage's DMA in two
+  // halves issued one MFMA step apart: the texture unit takes a stage's
+  // fetches (64 KB for a 256x256 16-bit tile) at about 64 B per clock, and
+  // a burst of them fills its command queue, which stalls the issuing wave
+  // and with it that wave's MFMAs behind the blocked load.
+  constexpr bool SPLIT_DMA = S == 2 && AMODE == MODE_K && BMODE == MODE_K && LA::kExactPer && LB::kExactPer;
+  constexpr int HA = LA::kGlobalLoads / 2, HB = LB::kGlobalLoads / 2;  // first halves
+
   // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage,
   // S LDS buffers used as a ring:
   //   step 0-2: the LDS reads of step s+1 are in flight while step s's MFMAs
   //             issue;
+  //   step 0:   (split DMA) the second half of stage kt+1's DMA;
   //   step 2:   register loaders write stage kt+1 into the next buffer;
   //   step 3:   wait until stage kt+1 has landed, one barrier, then the next
-  //             stage's step-0 reads, the DMA of stage kt+S into the buffer
-  //             just released and the register loaders' global reads of stage
-  //             kt+2 all overlap this stage's last MFMAs.
+  //             stage's step-0 reads, the DMA of stage kt+S (its first half
+  //             with split DMA) into the buffer just released and the
+  //             register loaders' global reads of stage kt+2 all overlap this
+  //             stage's last MFMAs.
   // A buffer is refilled only after the barrier that follows its last read,
   // and read only after the barrier that follows its fill.  The DMA of a stage
-  // has S-1 stages of MFMAs to land; vector memory reads complete in issue
-  // order, so "at most (S-2) stages of DMA outstanding" means stage kt+1 has
-  // landed.  The body is branch-free: past the last stage every global read
-  // is out of range (zeros) and the extra LDS writes land in a buffer nothing
-  // reads.
+  // has S-1 stages of MFMAs to land (three steps for a split second half);
+  // vector memory reads complete in issue order, so "at most (S-2) stages of
+  // DMA outstanding" means stage kt+1 has landed.  The body is branch-free:
+  // past the last stage every global read is out of range (zeros) and the
+  // extra LDS writes land in a buffer nothing reads.
   la.issue(kt0, smem);
   lb.issue(kt0, smem + BM * kRowBytes);
   la.commit(smem);
   lb.commit(smem + BM * kRowBytes);
+  if constexpr (SPLIT_DMA) {
+    la.template issue_part<0, HA>(kt0 + 1, smem + STAGE);
+    lb.template issue_part<0, HB>(kt0 + 1, smem + STAGE + BM * kRowBytes);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (HA + HB));  // stage kt0 landed
+  } else {
 #pragma unroll
-  for (int d = 1; d < S; ++d) {
-    if constexpr (LA::kDirect) la.issue(kt0 + d, smem + d * STAGE);
-    if constexpr (LB::kDirect) lb.issue(kt0 + d, smem + d * STAGE + BM * kRowBytes);
+    for (int d = 1; d < S; ++d) {
+      if constexpr (LA::kDirect) la.issue(kt0 + d, smem + d * STAGE);
+      if constexpr (LB::kDirect) lb.issue(kt0 + d, smem + d * STAGE + BM * kRowBytes);
+    }
+    if constexpr (!LA::kDirect) la.issue(kt0 + 1, nullptr);
+    if constexpr (!LB::kDirect) lb.issue(kt0 + 1, nullptr);
+    if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stages kt0, kt0+1 landed
   }
-  if constexpr (!LA::kDirect) la.issue(kt0 + 1, nullptr);
-  if constexpr (!LB::kDirect) lb.issue(kt0 + 1, nullptr);
-  if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stages kt0, kt0+1 landed
   __syncthreads();
   Frags<TM, TN> f0, f1;
   load_frags(f0, smem, smem + BM * kRowBytes, wr0, wc0, lr, h * 4);
@@ -811,8 +830,13 @@ void fused_gemm_kernel(GemmArgs p) {
     char* cur = smem + bi * STAGE;
     char* nxt = smem + bn * STAGE;
     load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
+    if constexpr (SPLIT_DMA) {
+      // nxt (stage kt+1) was released at the previous iteration's barrier.
+      la.template issue_part<HA, LA::kGlobalLoads>(kt + 1, nxt);
+      lb.template issue_part<HB, LB::kGlobalLoads>(kt + 1, nxt + BM * kRowBytes);
+    }
     mma_frags<DT>(f0, acc);
-    sched_step<NM, NR, 0, 0>();
+    sched_step<NM, NR, 0, SPLIT_DMA ? NG_DIRECT - HA - HB : 0>();
     load_frags(f0, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 2);
     mma_frags<DT>(f1, acc);
     sched_step<NM, NR, 0, 0>();
@@ -824,12 +848,17 @@ void fused_gemm_kernel(GemmArgs p) {
     if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stage kt+1 landed
     __syncthreads();
     load_frags(f0, nxt, nxt + BM * kRowBytes, wr0, wc0, lr, h * 4);
-    if constexpr (LA::kDirect) la.issue(kt + S, cur);
-    if constexpr (LB::kDirect) lb.issue(kt + S, cur + BM * kRowBytes);
-    if constexpr (!LA::kDirect) la.issue(kt + 2, nullptr);
-    if constexpr (!LB::kDirect) lb.issue(kt + 2, nullptr);
+    if constexpr (SPLIT_DMA) {
+      la.template issue_part<0, HA>(kt + S, cur);
+      lb.template issue_part<0, HB>(kt + S, cur + BM * kRowBytes);
+    } else {
+      if constexpr (LA::kDirect) la.issue(kt + S, cur);
+      if constexpr (LB::kDirect) lb.issue(kt + S, cur + BM * kRowBytes);
+      if constexpr (!LA::kDirect) la.issue(kt + 2, nullptr);
+      if constexpr (!LB::kDirect) lb.issue(kt + 2, nullptr);
+    }
     mma_frags<DT>(f1, acc);
-    sched_step<NM, NR, 0, NG_DIRECT + NG_REG>();
+    sched_step<NM, NR, 0, SPLIT_DMA ? HA + HB : NG_DIRECT + NG_REG>();
     bi = bn;
   }
   __syncthreads();
