@@ -66,7 +66,10 @@ def _time_launches(launch, steps: int, warmup: int):
 
 
 def gemm_workload(name, m, n, k, dtype, *, steps, warmup, act="gelu", bias=True, a_std=None, w_std=None,
-                  config=None):
+                  config=None, vendor=False):
+    """One GEMM workload through this library's kernel, or with `vendor` through torch's
+    library GEMM (hipBLASLt: `torch.matmul(A, W^T, out=)`, no bias or activation) on the
+    same operands, as a reference point for the counters."""
     from forgeml_amd import kernels
 
     dev = torch.device("cuda", 0)
@@ -75,8 +78,12 @@ def gemm_workload(name, m, n, k, dtype, *, steps, warmup, act="gelu", bias=True,
     cfg = config or kernels.DEFAULT_CONFIG
     resolved = kernels.resolve_config(m, n, k, dtype, cfg)
 
-    def launch():
-        kernels.matmul(a, b, bvec, activation=act, out=out, config=cfg)
+    if vendor:
+        def launch():
+            torch.matmul(a, b, out=out)
+    else:
+        def launch():
+            kernels.matmul(a, b, bvec, activation=act, out=out, config=cfg)
 
     wall_ms, per_launch = _time_launches(launch, steps, warmup)
     avg_ms = statistics.fmean(per_launch)
@@ -87,9 +94,10 @@ def gemm_workload(name, m, n, k, dtype, *, steps, warmup, act="gelu", bias=True,
         "workload": name,
         "shape": [m, n, k],
         "dtype": DTYPE_NAMES[dtype],
-        "activation": act,
-        "bias": bias,
-        "tile": [resolved.block_m, resolved.block_n, resolved.block_k, resolved.num_waves],
+        "kernel": "torch.matmul (vendor library GEMM, no epilogue)" if vendor else "forgeml_hip fused GEMM",
+        "activation": "none" if vendor else act,
+        "bias": bias and not vendor,
+        "tile": None if vendor else [resolved.block_m, resolved.block_n, resolved.block_k, resolved.num_waves],
         "ms_per_step": wall_ms,
         "kernel_ms_avg": avg_ms,
         "kernel_ms_min": min(per_launch),
@@ -282,6 +290,8 @@ def main() -> int:
                     help="run one extra GEMM workload only (for profiling) and print its record")
     ap.add_argument("--tile", default=None, metavar="BMxBNxWAVES",
                     help="with --only: force this tile configuration instead of the shape heuristic")
+    ap.add_argument("--vendor", action="store_true",
+                    help="with --only: time torch's library GEMM (hipBLASLt) on the same operands instead")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -306,7 +316,7 @@ def main() -> int:
                 return 2
             config = matches[0]
         print(json.dumps(gemm_workload(args.only, *EXTRA_GEMMS[args.only], steps=args.steps, warmup=args.warmup,
-                                       config=config, **EXTRA_KW[args.only])), flush=True)
+                                       config=config, vendor=args.vendor, **EXTRA_KW[args.only])), flush=True)
         return 0
     if args.calibrate_copy:
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")

@@ -23,7 +23,10 @@
 //    16-byte vectors along M/N and transpose VEC x VEC blocks in registers;
 //    anything else uses element loads.
 //  * Waves compute 32x32 MFMA blocks: v_mfma_f32_32x32x2_f32 (IEEE fp32 path)
-//    or v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulation.
+//    or v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulation; four-wave
+//    16-bit tiles up to 128x128 with both operands K-contiguous use 16x16
+//    blocks of v_mfma_f32_16x16x32_{bf16,f16}, whose LDS rows use a swizzle
+//    that repeats every 16 rows.
 //  * The epilogue rounds to the output dtype, adds the bias in fp32, rounds
 //    again, applies GELU (erf or tanh) or clamp_min(x,0) in registers and
 //    stores once.
@@ -34,9 +37,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace forgeml {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -82,6 +88,17 @@ struct DTraits {
 // Byte offset of logical 16-byte chunk `c` of LDS row `r`.
 __device__ __forceinline__ int lds_off(int r, int c) {
   return r * kRowBytes + (((c ^ r ^ (r >> 3)) & 7) << 4);
+}
+
+// Swizzle of the 16x16x32 MFMA path: (r & 7) ^ ((r >> 3) & 1) repeats every
+// 16 rows, so all fragments of a step (16-row blocks) sit at one per-lane base
+// plus immediate offsets; 8 consecutive rows of one chunk still cover 8
+// distinct 16-byte bank groups, and 16 rows 16 groups of a 256-byte line.
+__device__ __forceinline__ int lds_swz16(int r) {
+  return (r & 7) ^ ((r >> 3) & 1);
+}
+__device__ __forceinline__ int lds_off16(int r, int c) {
+  return r * kRowBytes + ((c ^ lds_swz16(r)) << 4);
 }
 
 // ---------------------------------------------------------------------------
@@ -204,7 +221,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // buffer_load_dwordx4 ... lds of a wave writes a contiguous 1 KB block (lane
 // L at byte 16*L) = 8 LDS rows; each lane fetches the chunk whose swizzled
 // LDS position is its own slot.
-template <int DT, int ROWS, int NT>
+template <int DT, int ROWS, int NT, bool SW16 = false>
 struct LoaderK {
   static constexpr bool kDirect = true;
   static constexpr int BLOCKS = ROWS / 8;
@@ -212,10 +229,17 @@ struct LoaderK {
   static constexpr int PER = (BLOCKS + NWAVES - 1) / NWAVES;
   static constexpr int kGlobalLoads = PER, kLdsWrites = 0;  // per thread per stage
   static constexpr bool kExactPer = BLOCKS % NWAVES == 0;    // every wave issues PER DMAs
+  // With the 16-row swizzle a lane's chunk is the same in every block it
+  // loads when the wave count is even (block parity = wave parity).
+  static constexpr bool kOneChunk = SW16 && NWAVES % 2 == 0;
   __amdgpu_buffer_rsrc_t rsrc;
   int kbytes;
-  uint32_t voff[PER];  // this lane's byte offset in stage 0, or out of range
-  int kchunk[PER];     // byte offset of this lane's chunk within a stage
+  // This lane's byte offset in stage 0 per block, or out of range.  With one
+  // chunk, only block 0's offset and row are kept: block i is i * NWAVES * 8
+  // rows further (fewer registers next to the 16x16x32 path's fragments).
+  uint32_t voff[kOneChunk ? 1 : PER];
+  int kchunk[kOneChunk ? 1 : PER];  // byte offset of this lane's chunk within a stage
+  int vrow, valid, step_bytes;      // one chunk: block 0's row; rows in range; bytes per block step
 
   __device__ __forceinline__ void init(const char* b, int64_t s_mn, int64_t /*s_k*/, int r0, int nrows, int k) {
     const int ld_bytes = (int)(s_mn * DTraits<DT>::ESZ);
@@ -228,10 +252,21 @@ struct LoaderK {
     for (int i = 0; i < PER; ++i) {
       const int blk = wave + i * NWAVES;
       const int r = blk * 8 + (lane >> 3);
-      const int c = (lane ^ r ^ (r >> 3)) & 7;  // logical chunk stored at physical slot lane&7
-      kchunk[i] = c * 16;
-      voff[i] = (r < valid_rows && blk < BLOCKS) ? (uint32_t)(r * ld_bytes + c * 16) : kOutOfRange;
+      // logical chunk stored at physical slot lane&7
+      const int c = SW16 ? ((lane & 7) ^ lds_swz16(r)) : ((lane ^ r ^ (r >> 3)) & 7);
+      if constexpr (kOneChunk) {
+        if (i == 0) {
+          kchunk[0] = c * 16;
+          voff[0] = (uint32_t)(r * ld_bytes + c * 16);
+          vrow = r;
+        }
+      } else {
+        kchunk[i] = c * 16;
+        voff[i] = (r < valid_rows && blk < BLOCKS) ? (uint32_t)(r * ld_bytes + c * 16) : kOutOfRange;
+      }
     }
+    valid = valid_rows;
+    step_bytes = NWAVES * 8 * ld_bytes;
   }
   // DMAs [P0, P1) of this wave's PER for stage kt.  Stage kt's K offset goes
   // in the scalar offset; lanes past the K tail get an out-of-range vector
@@ -246,7 +281,13 @@ struct LoaderK {
     for (int i = P0; i < P1; ++i) {
       const int blk = wave + i * NWAVES;  // uniform per wave
       if (BLOCKS % NWAVES == 0 || blk < BLOCKS) {
-        const uint32_t off = kchunk[i] < klimit ? voff[i] : kOutOfRange;
+        uint32_t off;
+        if constexpr (kOneChunk) {
+          const bool ok = vrow + i * NWAVES * 8 < valid && blk < BLOCKS && kchunk[0] < klimit;
+          off = ok ? voff[0] + (uint32_t)(i * step_bytes) : kOutOfRange;
+        } else {
+          off = kchunk[i] < klimit ? voff[i] : kOutOfRange;
+        }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(stage + blk * 1024), 16, off, kbase, 0, 0);
       }
     }
@@ -485,16 +526,17 @@ constexpr int lds_stages() {
                                                                                                               : 2;
 }
 
-template <int MODE, int DT, int ROWS, int NT>
+// SW16: the operand is read by the 16x16x32 path (lds_off16 layout; K-contiguous only).
+template <int MODE, int DT, int ROWS, int NT, bool SW16 = false>
 struct LoaderSel;
+template <int DT, int ROWS, int NT, bool SW16>
+struct LoaderSel<MODE_K, DT, ROWS, NT, SW16> { using type = LoaderK<DT, ROWS, NT, SW16>; };
 template <int DT, int ROWS, int NT>
-struct LoaderSel<MODE_K, DT, ROWS, NT> { using type = LoaderK<DT, ROWS, NT>; };
+struct LoaderSel<MODE_MN, DT, ROWS, NT, false> { using type = LoaderMN<DT, ROWS, NT>; };
 template <int DT, int ROWS, int NT>
-struct LoaderSel<MODE_MN, DT, ROWS, NT> { using type = LoaderMN<DT, ROWS, NT>; };
+struct LoaderSel<MODE_G, DT, ROWS, NT, false> { using type = LoaderG<DT, ROWS, NT>; };
 template <int DT, int ROWS, int NT>
-struct LoaderSel<MODE_G, DT, ROWS, NT> { using type = LoaderG<DT, ROWS, NT>; };
-template <int DT, int ROWS, int NT>
-struct LoaderSel<MODE_K4, DT, ROWS, NT> { using type = LoaderK4<DT, ROWS, NT>; };
+struct LoaderSel<MODE_K4, DT, ROWS, NT, false> { using type = LoaderK4<DT, ROWS, NT>; };
 
 // ---------------------------------------------------------------------------
 // MFMA over one LDS stage.  Lane l of a wave covers M (or N) index l%32 of a
@@ -537,6 +579,43 @@ __device__ __forceinline__ void mma_frags(const Frags<TM, TN>& f, f32x16 (&acc)[
                                                               __builtin_bit_cast(bf16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
       } else {
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, f.a[tm]),
+                                                             __builtin_bit_cast(f16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Four-wave 16-bit tiles up to 128x128 fed by DMA use
+// v_mfma_f32_16x16x32_{bf16,f16} instead: a stage is two MFMA steps of 32 K
+// elements, lane l covering M (or N) index l%16 of a 16x16 block and K chunk
+// l/16 of the step (logical chunk 4*step + l/16 of its row).  A step is
+// twice as many MFMA cycles as with the 32x32 shape (32 K instead of 16) for
+// the same LDS bytes per K, so the next step's fragment reads have twice as
+// long to return; its fragments take twice the registers.  TM and TN count
+// 16-row and 16-column blocks here.
+// `ao`/`bo`: this lane's byte offset of the step's chunk in its first A / B
+// row (lds_off16 of row wr0 + l%16 / wc0 + l%16); block t is 16 rows further.
+template <int TM, int TN>
+__device__ __forceinline__ void load_frags16(Frags<TM, TN>& f, const char* lda, const char* ldb, int ao, int bo) {
+  f.a[0] = *(const u32x4*)(lda + ao);
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) f.b[tn] = *(const u32x4*)(ldb + bo + tn * 16 * kRowBytes);
+#pragma unroll
+  for (int tm = 1; tm < TM; ++tm) f.a[tm] = *(const u32x4*)(lda + ao + tm * 16 * kRowBytes);
+}
+
+template <int DT, int TM, int TN>
+__device__ __forceinline__ void mma_frags(const Frags<TM, TN>& f, f32x4 (&acc)[TM][TN]) {
+  static_assert(DT != DT_F32, "the 16x16x32 path is for 16-bit inputs");
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      if constexpr (DT == DT_BF16) {
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a[tm]),
+                                                              __builtin_bit_cast(bf16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
+      } else {
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, f.a[tm]),
                                                              __builtin_bit_cast(f16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
       }
     }
@@ -614,14 +693,37 @@ __device__ __forceinline__ void wave_sync() {
 // Order of operations follows the reference kernel (src/forgeml/_triton.py:
 // 43-57): round to the output dtype, add the bias in fp32, round again,
 // activate, store.
-template <int DT, int ACT, int TM, int TN, bool INTERIOR>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[TM][TN], float* buf,
-                                         int row_base, int col_base, int lane) {
+// Writes 32-row band `tm` of a wave's accumulators to its LDS slice as
+// [32-column block][row][column] floats.  32x32 blocks: element i of lane l
+// is row 8*(i/4) + 4*(l/32) + i%4, column l%32.  16x16 blocks (two per band
+// row and column): element i of lane l is row 4*(l/16) + i, column l%16.
+template <int TM, int TN>
+__device__ __forceinline__ void write_band(const f32x16 (&acc)[TM][TN], int tm, float* buf, int lane) {
+  const int lr = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) buf[(tn * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[tm][tn][i];
+}
+template <int TM2, int TN2>
+__device__ __forceinline__ void write_band(const f32x4 (&acc)[TM2][TN2], int tm, float* buf, int lane) {
+  const int c16 = lane & 15, r4 = (lane >> 4) * 4;
+#pragma unroll
+  for (int hm = 0; hm < 2; ++hm)
+#pragma unroll
+    for (int tn = 0; tn < TN2; ++tn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        buf[((tn >> 1) * 32 + hm * 16 + r4 + i) * 32 + (tn & 1) * 16 + c16] = acc[2 * tm + hm][tn][i];
+}
+
+template <int DT, int ACT, int TM, int TN, bool INTERIOR, class Acc>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, float* buf, int row_base, int col_base,
+                                         int lane) {
   constexpr int ESZ = DTraits<DT>::ESZ;
   constexpr int EPV = 16 / ESZ;      // outputs per lane per row segment
   constexpr int CPR = 32 / EPV;      // lanes per 32-column block row
   constexpr int SEGS = 32 * CPR / 64;  // row segments per lane per block
-  const int lr = lane & 31, h = lane >> 5;
   const int cq = (lane % CPR) * EPV;  // this lane's first column within a block
   const bool vec_ok = INTERIOR || ((p.n % EPV) == 0 && (((uintptr_t)p.c) & 15) == 0);
   float bias[TN][EPV];
@@ -634,10 +736,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[
     }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) buf[(tn * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[tm][tn][i];
+    write_band(acc, tm, buf, lane);
     wave_sync();
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
@@ -704,9 +803,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const f32x16 (&acc)[
   }
 }
 
-template <int DT, int ACT, int TM, int TN>
-__device__ __forceinline__ void epilogue_dispatch(const GemmArgs& p, const f32x16 (&acc)[TM][TN], float* buf,
-                                                  int row_base, int col_base, int lane, bool interior) {
+template <int DT, int ACT, int TM, int TN, class Acc>
+__device__ __forceinline__ void epilogue_dispatch(const GemmArgs& p, const Acc& acc, float* buf, int row_base,
+                                                  int col_base, int lane, bool interior) {
   if (interior) epilogue<DT, ACT, TM, TN, true>(p, acc, buf, row_base, col_base, lane);
   else epilogue<DT, ACT, TM, TN, false>(p, acc, buf, row_base, col_base, lane);
 }
@@ -746,8 +845,16 @@ void fused_gemm_kernel(GemmArgs p) {
   const int nks = min((p.k * ESZ + kRowBytes - 1) / kRowBytes - kt0, p.kslice);
   const int kend = min(p.k, (kt0 + nks) * DTraits<DT>::BKE);
 
-  typename LoaderSel<AMODE, DT, BM, NT>::type la;
-  typename LoaderSel<BMODE, DT, BN, NT>::type lb;
+  // Four-wave 16-bit tiles up to 128x128 whose operands are both
+  // K-contiguous use 16x16x32 MFMAs, two steps per stage; the others 32x32
+  // MFMAs, four steps per stage (register loaders write LDS in step 2).  A
+  // 16x16x32 step holds twice the fragment registers of a 32x32 step: the
+  // 256x256 tiles have no room for them next to their accumulators.
+  constexpr bool M16 = DT != DT_F32 && AMODE == MODE_K && BMODE == MODE_K && WM * WN == 4 && BM * BN <= 128 * 128;
+  using LA = typename LoaderSel<AMODE, DT, BM, NT, M16>::type;
+  using LB = typename LoaderSel<BMODE, DT, BN, NT, M16>::type;
+  LA la;
+  LB lb;
   la.init(p.a, p.sam, p.sak, row0, p.m, kend);
   lb.init(p.b, p.sbn, p.sbk, col0, p.n, kend);
 
@@ -755,44 +862,51 @@ void fused_gemm_kernel(GemmArgs p) {
   const int wr0 = (wave / WN) * (TM * 32);
   const int wc0 = (wave % WN) * (TN * 32);
 
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.0f;
-
   const int lr = lane & 31, h = lane >> 5;
-  using LA = typename LoaderSel<AMODE, DT, BM, NT>::type;
-  using LB = typename LoaderSel<BMODE, DT, BN, NT>::type;
   constexpr bool ANY_DIRECT = LA::kDirect || LB::kDirect;
-  constexpr int NM = TM * TN * (DT == DT_F32 ? 4 : 1);  // MFMAs per step
-  constexpr int NR = TM + TN;                            // LDS reads per step
+  constexpr int NSTEP = M16 ? 2 : 4;
+  constexpr int FTM = M16 ? 2 * TM : TM, FTN = M16 ? 2 * TN : TN;  // operand fragments per step
+  using Acc = std::conditional_t<M16, f32x4[2 * TM][2 * TN], f32x16[TM][TN]>;
+  Acc acc = {};
+  constexpr int NM = FTM * FTN * (DT == DT_F32 ? 4 : 1);  // MFMAs per step
+  constexpr int NR = FTM + FTN;                            // LDS reads per step
   constexpr int NG_DIRECT = (LA::kDirect ? LA::kGlobalLoads : 0) + (LB::kDirect ? LB::kGlobalLoads : 0);
   constexpr int NG_REG = (LA::kDirect ? 0 : LA::kGlobalLoads) + (LB::kDirect ? 0 : LB::kGlobalLoads);
   constexpr int NW = LA::kLdsWrites + LB::kLdsWrites;
   constexpr int S = lds_stages<BM, BN, AMODE, BMODE>();
   static_assert(S == 2 || (LA::kDirect && LB::kDirect && LA::kExactPer && LB::kExactPer),
                 "rings deeper than two stages count DMA instructions per wave exactly");
+  using Fr = Frags<FTM, FTN>;
+  // 16x16x32 path: per-lane offsets of the two steps' chunks (rows 16 apart
+  // share them).
+  const int ao0 = lds_off16(wr0 + (lane & 15), lane >> 4), bo0 = lds_off16(wc0 + (lane & 15), lane >> 4);
+  const int ao1 = lds_off16(wr0 + (lane & 15), 4 + (lane >> 4)), bo1 = lds_off16(wc0 + (lane & 15), 4 + (lane >> 4));
+  // Fragments of MFMA step `step` of the stage at `base`.
+  auto read_step = [&](Fr& f, const char* base, int step) {
+    if constexpr (M16) load_frags16(f, base, base + BM * kRowBytes, step ? ao1 : ao0, step ? bo1 : bo0);
+    else load_frags(f, base, base + BM * kRowBytes, wr0, wc0, lr, h * 4 + step);
+  };
 
-  // Two-stage rings of K-contiguous operands split each stage's DMA in two
-  // halves issued one MFMA step apart: the texture unit takes a stage's
-  // fetches (64 KB for a 256x256 16-bit tile) at about 64 B per clock, and
-  // a burst of them fills its command queue, which stalls the issuing wave
-  // and with it that wave's MFMAs behind the blocked load.
-  constexpr bool SPLIT_DMA = S == 2 && AMODE == MODE_K && BMODE == MODE_K && LA::kExactPer && LB::kExactPer;
+  // Two-stage rings of K-contiguous operands with four MFMA steps per stage
+  // split each stage's DMA in two halves issued one step apart: the texture
+  // unit takes a stage's fetches (64 KB for a 256x256 16-bit tile) at about
+  // 64 B per clock, and a burst of them fills its command queue, which
+  // stalls the issuing wave and with it that wave's MFMAs behind the blocked
+  // load.
+  constexpr bool SPLIT_DMA =
+      NSTEP == 4 && S == 2 && AMODE == MODE_K && BMODE == MODE_K && LA::kExactPer && LB::kExactPer;
   constexpr int HA = LA::kGlobalLoads / 2, HB = LB::kGlobalLoads / 2;  // first halves
 
-  // Software pipeline over K stages, 4 MFMA steps of 32 bytes of K per stage,
-  // S LDS buffers used as a ring:
-  //   step 0-2: the LDS reads of step s+1 are in flight while step s's MFMAs
-  //             issue;
+  // Software pipeline over K stages, NSTEP MFMA steps per stage, S LDS
+  // buffers used as a ring:
+  //   steps 0..NSTEP-2: the LDS reads of step s+1 are in flight while step
+  //             s's MFMAs issue;
   //   step 0:   (split DMA) the second half of stage kt+1's DMA;
-  //   step 2:   register loaders write stage kt+1 into the next buffer;
-  //   step 3:   wait until stage kt+1 has landed, one barrier, then the next
-  //             stage's step-0 reads, the DMA of stage kt+S (its first half
-  //             with split DMA) into the buffer just released and the
+  //   step 2:   (four steps) register loaders write stage kt+1 into the next
+  //             buffer;
+  //   last step: wait until stage kt+1 has landed, one barrier, then the
+  //             next stage's step-0 reads, the DMA of stage kt+S (its first
+  //             half with split DMA) into the buffer just released and the
   //             register loaders' global reads of stage kt+2 all overlap this
   //             stage's last MFMAs.
   // A buffer is refilled only after the barrier that follows its last read,
@@ -821,15 +935,15 @@ void fused_gemm_kernel(GemmArgs p) {
     if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stages kt0, kt0+1 landed
   }
   __syncthreads();
-  Frags<TM, TN> f0, f1;
-  load_frags(f0, smem, smem + BM * kRowBytes, wr0, wc0, lr, h * 4);
+  Fr f0, f1;
+  read_step(f0, smem, 0);
   int bi = 0;  // ring index of stage kt
   for (int it = 0; it < nks; ++it) {
     const int kt = kt0 + it;
     const int bn = bi + 1 == S ? 0 : bi + 1;
     char* cur = smem + bi * STAGE;
     char* nxt = smem + bn * STAGE;
-    load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 1);
+    read_step(f1, cur, 1);
     if constexpr (SPLIT_DMA) {
       // nxt (stage kt+1) was released at the previous iteration's barrier.
       la.template issue_part<HA, LA::kGlobalLoads>(kt + 1, nxt);
@@ -837,17 +951,19 @@ void fused_gemm_kernel(GemmArgs p) {
     }
     mma_frags<DT>(f0, acc);
     sched_step<NM, NR, 0, SPLIT_DMA ? NG_DIRECT - HA - HB : 0>();
-    load_frags(f0, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 2);
-    mma_frags<DT>(f1, acc);
-    sched_step<NM, NR, 0, 0>();
-    load_frags(f1, cur, cur + BM * kRowBytes, wr0, wc0, lr, h * 4 + 3);
-    if constexpr (!LA::kDirect) la.commit(nxt);
-    if constexpr (!LB::kDirect) lb.commit(nxt + BM * kRowBytes);
-    mma_frags<DT>(f0, acc);
-    sched_step<NM, NR, NW, 0>();
+    if constexpr (NSTEP == 4) {
+      read_step(f0, cur, 2);
+      mma_frags<DT>(f1, acc);
+      sched_step<NM, NR, 0, 0>();
+      read_step(f1, cur, 3);
+      if constexpr (!LA::kDirect) la.commit(nxt);
+      if constexpr (!LB::kDirect) lb.commit(nxt + BM * kRowBytes);
+      mma_frags<DT>(f0, acc);
+      sched_step<NM, NR, NW, 0>();
+    }
     if constexpr (ANY_DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70 | ((S - 2) * NG_DIRECT));  // stage kt+1 landed
     __syncthreads();
-    load_frags(f0, nxt, nxt + BM * kRowBytes, wr0, wc0, lr, h * 4);
+    read_step(f0, nxt, 0);
     if constexpr (SPLIT_DMA) {
       la.template issue_part<0, HA>(kt + S, cur);
       lb.template issue_part<0, HB>(kt + S, cur + BM * kRowBytes);

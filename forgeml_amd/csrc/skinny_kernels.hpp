@@ -35,7 +35,6 @@ constexpr int kSkinnyThreads = kSkinnyWaves * 64;
 constexpr int kSkinnyDepth = 4;     // chunks in flight per wave
 constexpr int kSkinnyMaxRows = 64;  // 16 * TM, TM <= 4
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 

@@ -20,5 +20,5 @@
 #define FORGEML_H16_TILES(X)       \
   X(256, 256, 2, 2, 1, 91, 91)     \
   X(128, 128, 2, 2, 2, 87, 80)     \
-  X(64, 64, 2, 2, 2, 55, 55)       \
+  X(64, 64, 2, 2, 2, 62, 62)       \
   X(256, 256, 2, 4, 1, 100, 100)
