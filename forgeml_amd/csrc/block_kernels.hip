@@ -185,24 +185,35 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e): softmax in base 2
 };
 
-constexpr int kAttnWaves = 4;
+// Two waves share a work item: wave w takes the item's key blocks kb with
+// kb % 2 == w and keeps its own online-softmax state (m, l, O); wave 1 hands
+// its state to wave 0 through LDS, which merges, normalises and transposes
+// the output, and both store it.  The split doubles the waves in flight
+// (one work item per wave left a quarter of the SIMDs idle on a transformer
+// block's heads) and halves each wave's serial chain of key blocks.
+constexpr int kAttnSplit = 2;
 
-// One wave: one work item of head (b, h).  A work item is query block qb
+// One workgroup: one work item of head (b, h).  A work item is query block qb
 // (rows [32*qb, 32*qb + 32)); with the causal mask it is the pair of blocks t
-// and nqb-1-t, whose key blocks add up to nqb+1 for every t, so all waves
-// carry the same work and none waits on the longest rows alone.
+// and nqb-1-t, whose key blocks add up to nqb+1 for every t, so all
+// workgroups carry the same work and none waits on the longest rows alone.
+// Two waves per SIMD at every head dim: at dim 96 that spills some
+// registers and is still faster than one wave per SIMD (76 vs 98 us on an
+// 8x12x512 causal problem).
 template <int D>
-__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) {
+__global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void attention_kernel(AttnArgs p) {
   static_assert(D % 32 == 0 && D <= 96, "head dim must be 32, 64 or 96");
   constexpr int NC = D / 8;   // 8-element chunks of the head dim
   constexpr int NB = D / 32;  // 32-row blocks of O^T
-  __shared__ float tr[kAttnWaves][32][D + 1];  // output transpose; odd row length: conflict-free column writes
+  __shared__ float tr[32][D + 1];        // merged output transpose; odd row length: conflict-free column writes
+  __shared__ float part[NB * 16][64];    // wave 1's unnormalised O^T, in its accumulator layout
+  __shared__ float part_ml[2][64];       // wave 1's running max and sum per lane
 
   const int lane = threadIdx.x & 63, half = lane >> 5, lc = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x * kAttnWaves + wave;
+  const int g = blockIdx.x;  // the grid is exactly one workgroup per work item
   const int nbh = p.batch * p.heads;
-  if (g >= nbh * p.nitems) return;  // whole wave; no workgroup barrier below
   const int t = g / nbh, bh = g % nbh;
   const int b = bh / p.heads, h = bh % p.heads;
   const int nrep = (p.causal && t != p.nqb - 1 - t) ? 2 : 1;
@@ -259,15 +270,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) 
     }
   };
 
-  // K of the next key block loads while this one computes; V loads at the
-  // start of its block and is needed only after S and the softmax.  (Holding
-  // the next block's V too costs more in register moves than it saves.)
-  u32x4 kf[NC], kn[NC];
-  load_k(0, kf);
-  for (int kb = 0; kb < nkb; ++kb) {
+  // K and V of a key block load at its start; V is needed only after S and
+  // the softmax.  Two waves per SIMD (the registers of a next-block prefetch
+  // would allow one) hide the K latency better than a prefetch does.
+  for (int kb = wave; kb < nkb; kb += kAttnSplit) {
+    u32x4 kf[NC];
     float vf[NB][16];
+    load_k(kb, kf);
     load_v(kb, vf);
-    load_k(kb + 1, kn);
 
     // S^T[key][query] for this block, as two independent MFMA chains (even
     // and odd dim chunks) so consecutive MFMAs do not wait on each other.
@@ -320,27 +330,43 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) 
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[nb][i], s[i], o[nb], 0, 0, 0);
 
-#pragma unroll
-    for (int c = 0; c < NC; ++c) kf[c] = kn[c];
   }
 
-  // Normalise, transpose through LDS (this wave's slice only), store rows.
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  // Merge the two waves' states (base-2 running max m, sum l, unnormalised
+  // O^T), normalise, transpose through LDS.  A wave that saw no visible key
+  // has m = -inf and contributes nothing.
+  if (wave == 1) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) tr[wave][lc][nb * 32 + 8 * (i >> 2) + 4 * half + (i & 3)] = o[nb][i] * inv;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int i = 0; i < 16; ++i) part[nb * 16 + i][lane] = o[nb][i];
+    part_ml[0][lane] = m;
+    part_ml[1][lane] = l;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float m1 = part_ml[0][lane], l1 = part_ml[1][lane];
+    const float mm = fmaxf(m, m1);
+    const float base = mm == -INFINITY ? 0.0f : mm;
+    const float a0 = m == -INFINITY ? 0.0f : exp2f(m - base);
+    const float a1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - base);
+    const float lt = l * a0 + l1 * a1;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        tr[lc][nb * 32 + 8 * (i >> 2) + 4 * half + (i & 3)] = (o[nb][i] * a0 + part[nb * 16 + i][lane] * a1) * inv;
+  }
+  __syncthreads();
   float* op = p.o + b * p.so[0] + h * p.so[1];
   constexpr int VPR = D / 4;  // 16-byte vectors per output row
-  for (int idx = lane; idx < 32 * VPR; idx += 64) {
+  for (int idx = threadIdx.x; idx < 32 * VPR; idx += kAttnSplit * 64) {
     const int r = idx / VPR, c4 = (idx % VPR) * 4;
     const int qi = q0 + r;
     if (qi < p.lq) {
       float* dst = op + (int64_t)qi * p.so[2] + c4;
-      const float4 val = make_float4(tr[wave][r][c4], tr[wave][r][c4 + 1], tr[wave][r][c4 + 2], tr[wave][r][c4 + 3]);
+      const float4 val = make_float4(tr[r][c4], tr[r][c4 + 1], tr[r][c4 + 2], tr[r][c4 + 3]);
       if (p.so[3] == 1 && (((uintptr_t)dst) & 15) == 0) {
         *(float4*)dst = val;
       } else {
@@ -351,18 +377,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs p) 
       }
     }
   }
-  // This wave's next item reuses the transpose buffer after these reads.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // The next query block reuses tr and part after these reads.
+  __syncthreads();
   }
 }
 
 template <int D>
 static int launch_attention(const AttnArgs& p, hipStream_t stream) {
-  const int64_t waves = (int64_t)p.batch * p.heads * p.nitems;
-  hipLaunchKernelGGL((attention_kernel<D>), dim3((unsigned)((waves + kAttnWaves - 1) / kAttnWaves)),
-                     dim3(kAttnWaves * 64), 0, stream, p);
+  const int64_t items = (int64_t)p.batch * p.heads * p.nitems;
+  hipLaunchKernelGGL((attention_kernel<D>), dim3((unsigned)items), dim3(kAttnSplit * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FORGEML_EHIP, "attention launch failed: %s", hipGetErrorString(e));
   return FORGEML_OK;
@@ -423,7 +446,7 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
       ((lk - 1) * sv[2] + dim) * 4 >= ((int64_t)1 << 31))
     return set_error(FORGEML_EINVAL, "attention: a (batch, head) slice exceeds 2 GiB");
   const int64_t nqb = (lq + 31) / 32;
-  if (batch * heads * nqb > INT_MAX / kAttnWaves) return set_error(FORGEML_EINVAL, "attention: too many query blocks");
+  if (batch * heads * nqb > INT_MAX) return set_error(FORGEML_EINVAL, "attention: too many query blocks");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(FORGEML_EINVAL, "attention: scale must be finite and positive");
   AttnArgs p;
   p.q = (const float*)q;
