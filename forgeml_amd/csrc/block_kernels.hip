@@ -185,13 +185,15 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e): softmax in base 2
 };
 
-// Two waves share a work item: wave w takes the item's key blocks kb with
-// kb % 2 == w and keeps its own online-softmax state (m, l, O); wave 1 hands
-// its state to wave 0 through LDS, which merges, normalises and transposes
-// the output, and both store it.  The split doubles the waves in flight
-// (one work item per wave left a quarter of the SIMDs idle on a transformer
-// block's heads) and halves each wave's serial chain of key blocks.
-constexpr int kAttnSplit = 2;
+// Four waves share a work item: wave w takes the item's key blocks kb with
+// kb % 4 == w and keeps its own online-softmax state (m, l, O); waves 1-3
+// hand their states to wave 0 through LDS, which merges, normalises and
+// transposes the output, and all four store it.  The split multiplies the
+// waves in flight (one work item per wave left a quarter of the SIMDs idle
+// on a transformer block's heads) and shortens each wave's serial chain of
+// key blocks.  Measured against two waves per item: -17 % on full
+// attention at 8x12x512, -3 % causal, +3 % on a 1024-long causal problem.
+constexpr int kAttnSplit = 4;
 
 // One workgroup: one work item of head (b, h).  A work item is query block qb
 // (rows [32*qb, 32*qb + 32)); with the causal mask it is the pair of blocks t
@@ -207,8 +209,8 @@ void attention_kernel(AttnArgs p) {
   constexpr int NC = D / 8;   // 8-element chunks of the head dim
   constexpr int NB = D / 32;  // 32-row blocks of O^T
   __shared__ float tr[32][D + 1];        // merged output transpose; odd row length: conflict-free column writes
-  __shared__ float part[NB * 16][64];    // wave 1's unnormalised O^T, in its accumulator layout
-  __shared__ float part_ml[2][64];       // wave 1's running max and sum per lane
+  __shared__ float part[kAttnSplit - 1][NB * 16][64];  // waves 1.. unnormalised O^T, accumulator layout
+  __shared__ float part_ml[kAttnSplit - 1][2][64];     // their running max and sum per lane
 
   const int lane = threadIdx.x & 63, half = lane >> 5, lc = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -332,31 +334,43 @@ void attention_kernel(AttnArgs p) {
 
   }
 
-  // Merge the two waves' states (base-2 running max m, sum l, unnormalised
-  // O^T), normalise, transpose through LDS.  A wave that saw no visible key
-  // has m = -inf and contributes nothing.
-  if (wave == 1) {
+  // Merge the waves' states (base-2 running max m, sum l, unnormalised O^T):
+  // each is rescaled by 2^(m_w - max), summed in wave order, normalised and
+  // transposed through LDS.  A wave that saw no visible key has m = -inf and
+  // contributes nothing.
+  if (wave > 0) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) part[nb * 16 + i][lane] = o[nb][i];
-    part_ml[0][lane] = m;
-    part_ml[1][lane] = l;
+      for (int i = 0; i < 16; ++i) part[wave - 1][nb * 16 + i][lane] = o[nb][i];
+    part_ml[wave - 1][0][lane] = m;
+    part_ml[wave - 1][1][lane] = l;
   }
   __syncthreads();
   if (wave == 0) {
-    const float m1 = part_ml[0][lane], l1 = part_ml[1][lane];
-    const float mm = fmaxf(m, m1);
+    float mm = m;
+#pragma unroll
+    for (int w = 0; w < kAttnSplit - 1; ++w) mm = fmaxf(mm, part_ml[w][0][lane]);
     const float base = mm == -INFINITY ? 0.0f : mm;
     const float a0 = m == -INFINITY ? 0.0f : exp2f(m - base);
-    const float a1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - base);
-    const float lt = l * a0 + l1 * a1;
+    float aw[kAttnSplit - 1];
+    float lt = l * a0;
+#pragma unroll
+    for (int w = 0; w < kAttnSplit - 1; ++w) {
+      const float mw = part_ml[w][0][lane];
+      aw[w] = mw == -INFINITY ? 0.0f : exp2f(mw - base);
+      lt += part_ml[w][1][lane] * aw[w];
+    }
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        tr[lc][nb * 32 + 8 * (i >> 2) + 4 * half + (i & 3)] = (o[nb][i] * a0 + part[nb * 16 + i][lane] * a1) * inv;
+      for (int i = 0; i < 16; ++i) {
+        float v = o[nb][i] * a0;
+#pragma unroll
+        for (int w = 0; w < kAttnSplit - 1; ++w) v += part[w][nb * 16 + i][lane] * aw[w];
+        tr[lc][nb * 32 + 8 * (i >> 2) + 4 * half + (i & 3)] = v * inv;
+      }
   }
   __syncthreads();
   float* op = p.o + b * p.so[0] + h * p.so[1];
