@@ -7,9 +7,10 @@
 // for A and B both K-contiguous (A row-major, B = W^T of an nn.Linear weight).
 //
 // Design:
-//  * A workgroup owns 16 output columns and every row; M is padded to
-//    16*TM rows (TM <= 4) for v_mfma_f32_16x16x4_f32 (fp32) or
-//    v_mfma_f32_16x16x32_{bf16,f16} (16-bit), instead of to a 64-row tile.
+//  * A workgroup owns 16 output columns and 16*TM rows (TM <= 4): rows are
+//    padded to 16 for v_mfma_f32_16x16x4_f32 (fp32) or
+//    v_mfma_f32_16x16x32_{bf16,f16} (16-bit), instead of to a 64-row tile,
+//    and split over workgroups when the column groups alone leave CUs idle.
 //  * Its 8 waves split K.  Each wave streams its K range in chunks of one
 //    16-byte vector per lane per operand (16 fp32 or 32 bf16 of K), straight
 //    from global memory into registers, with 4 chunks in flight: no LDS
@@ -99,9 +100,11 @@ __device__ __forceinline__ void skinny_store(const GemmArgs& p, float v, int row
   store_from_f32<DT>(p.c + ((int64_t)row * p.n + col) * ESZ, x);
 }
 
-// Grid: ceil(N / 16) workgroups of kSkinnyThreads.  The host guarantees
-// M <= 16 * TM, both operands K-contiguous (sak = sbk = 1) with the alignment
-// LW needs, and 32-bit byte offsets for both operands.
+// Grid: ceil(N / 16) x ceil(M / (16 * TM)) workgroups of kSkinnyThreads;
+// workgroup (x, y) owns columns [16x, 16x + 16) of rows [16*TM*y,
+// 16*TM*(y + 1)).  The host guarantees M <= 64, both operands K-contiguous
+// (sak = sbk = 1) with the alignment LW needs, and 32-bit byte offsets for
+// both operands.
 template <int DT, int TM, int LW>
 __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p) {
   constexpr int ESZ = DTraits<DT>::ESZ;
@@ -113,6 +116,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.y * 16 * TM;
   const int j = lane & 15, kq = lane >> 4;
 
   // This wave's chunks [c0, c1) of the K dimension.
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p)
   uint32_t a_row[TM];
 #pragma unroll
   for (int mt = 0; mt < TM; ++mt) {
-    const int row = mt * 16 + j;
+    const int row = m0 + mt * 16 + j;
     a_row[mt] = row < p.m ? (uint32_t)((int64_t)row * p.sam * ESZ) : kOutOfRange;
   }
   const uint32_t b_row = j < ncols ? (uint32_t)((int64_t)j * p.sbn * ESZ) : kOutOfRange;
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p)
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < kSkinnyWaves; ++w) v += red[w][mt][src][r];
-    const int row = mt * 16 + i, col = n0 + jj;
+    const int row = m0 + mt * 16 + i, col = n0 + jj;
     if (row < p.m && col < p.n) {
       switch (p.act) {
         case ACT_GELU_ERF: skinny_store<DT, ACT_GELU_ERF>(p, v, row, col); break;
