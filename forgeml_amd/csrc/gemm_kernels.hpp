@@ -565,16 +565,25 @@ __device__ __forceinline__ void load_frags(Frags<TM, TN>& f, const char* lda, co
 
 template <int DT, int TM, int TN>
 __device__ __forceinline__ void mma_frags(const Frags<TM, TN>& f, f32x16 (&acc)[TM][TN]) {
+  if constexpr (DT == DT_F32) {
+    // The 4 K elements of the chunk outermost: consecutive MFMAs go to
+    // different accumulator blocks, and each block still adds its K elements
+    // in the same order (bit-identical results; about 1 % faster on 4096^3).
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(f.a[tm][j]), __uint_as_float(f.b[tn][j]),
+                                                             acc[tm][tn], 0, 0, 0);
+    return;
+  }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
-      if constexpr (DT == DT_F32) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(f.a[tm][j]), __uint_as_float(f.b[tn][j]),
-                                                             acc[tm][tn], 0, 0, 0);
-      } else if constexpr (DT == DT_BF16) {
+      if constexpr (DT == DT_BF16) {
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, f.a[tm]),
                                                               __builtin_bit_cast(bf16x8, f.b[tn]), acc[tm][tn], 0, 0, 0);
       } else {
