@@ -67,7 +67,7 @@ def lib():
     return _native.load()
 
 
-@settings(max_examples=400, deadline=None)
+@settings(max_examples=400, deadline=None, derandomize=True, database=None)
 @given(p=problems())
 def test_plan_invariants(lib, p):
     m, n, k, dtype, esz, sam, sak, sbk, sbn, _, _ = p
@@ -97,7 +97,7 @@ def test_plan_invariants(lib, p):
     assert _plan(lib, p, cid) == (rc, (cid, splits, ws, kind))
 
 
-@settings(max_examples=300, deadline=None)
+@settings(max_examples=300, deadline=None, derandomize=True, database=None)
 @given(m=st.integers(1, 8192), n=st.integers(1, 8192), kv=st.integers(1, 2048),
        dt=st.sampled_from(DTYPES))
 def test_select_config_matches_the_plan_for_aligned_k_contiguous_operands(lib, m, n, kv, dt):
