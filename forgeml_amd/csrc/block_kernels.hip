@@ -10,9 +10,10 @@
 // reductions in a fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
 // fp32, rounded once to the output dtype.
 //
-// Attention (fp32, head dim D of 32, 64 or 96): flash-style,
-// one wave per 32 query rows, streaming 32-key blocks with an online softmax.
-// The wave computes S^T = K Q^T on v_mfma_f32_32x32x2_f32, so that each lane
+// Attention (fp32, head dim D of 32, 64 or 96): flash-style, four waves per
+// 32 query rows, each streaming every fourth 32-key block with an online
+// softmax, their states merged at the end.  A wave computes S^T = K Q^T on
+// v_mfma_f32_32x32x2_f32, so that each lane
 // owns one query column of S^T: the softmax row statistics are a reduction
 // over the lane's 16 accumulator values plus one exchange with the other half
 // wave, and the lane's probabilities are already the B operand of
@@ -159,11 +160,12 @@ static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
   constexpr int VEC = 16 / DTraits<DT>::ESZ;
   const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
   const int per_lane = (p.cols + 64 * VEC - 1) / (64 * VEC);
-  if (!vec || per_lane > 8) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
+  if (!vec || per_lane > 16) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
   else if (per_lane <= 1) hipLaunchKernelGGL((layer_norm_kernel<DT, 1>), grid, block, 0, stream, p);
   else if (per_lane <= 2) hipLaunchKernelGGL((layer_norm_kernel<DT, 2>), grid, block, 0, stream, p);
   else if (per_lane <= 4) hipLaunchKernelGGL((layer_norm_kernel<DT, 4>), grid, block, 0, stream, p);
-  else hipLaunchKernelGGL((layer_norm_kernel<DT, 8>), grid, block, 0, stream, p);
+  else if (per_lane <= 8) hipLaunchKernelGGL((layer_norm_kernel<DT, 8>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((layer_norm_kernel<DT, 16>), grid, block, 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FORGEML_EHIP, "layer_norm launch failed: %s", hipGetErrorString(e));
   return FORGEML_OK;
