@@ -6,8 +6,10 @@
 // transformer block between the GEMMs (src/forgeml/neural.py:18-53).
 //
 // LayerNorm: one wave per row; the row is held in registers as 16-byte
-// vectors, mean and variance are two passes over those registers with wave
-// reductions in a fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
+// vectors (up to 16 per lane; wider aligned rows spread over a workgroup of
+// 256 or 1024 threads, and past that are read three times as vectors), mean
+// and variance are two passes over those registers with reductions in a
+// fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
 // fp32, rounded once to the output dtype.
 //
 // Attention (fp32, head dim D of 32, 64 or 96): flash-style, four waves per
@@ -64,6 +66,34 @@ __device__ __forceinline__ void unpack16(const u32x4& w, float (&out)[16 / DTrai
   }
 }
 
+// y[c0 .. c0+VEC) = (v - mean) * rstd (* w + b), one 16-byte store.
+template <int DT>
+__device__ __forceinline__ void ln_store_vec(const LnArgs& p, char* yr, int64_t c0, const float* v, float mean,
+                                             float rstd) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  constexpr int VEC = 16 / ESZ;
+  float o[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) o[e] = (v[e] - mean) * rstd;
+  if (p.w != nullptr) {
+    // Weight and bias as 16-byte vectors, like the row.
+    float wv[VEC], bv[VEC];
+    unpack16<DT>(*(const u32x4*)(p.w + c0 * ESZ), wv);
+    unpack16<DT>(*(const u32x4*)(p.b + c0 * ESZ), bv);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = o[e] * wv[e] + bv[e];
+  }
+  u32x4 w;
+  if constexpr (ESZ == 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(o[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack2<DT>(o[2 * e], o[2 * e + 1]);
+  }
+  *(u32x4*)(yr + c0 * ESZ) = w;
+}
+
 // Row held in registers: VPL 16-byte vectors per lane.
 template <int DT, int VPL>
 __global__ __launch_bounds__(256) void layer_norm_kernel(LnArgs p) {
@@ -105,32 +135,111 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LnArgs p) {
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c0 = (lane + 64 * i) * VEC;
-    if (c0 < p.cols) {
-      float o[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] - mean) * rstd;
-      if (p.w != nullptr) {
-        // Weight and bias as 16-byte vectors, like the row.
-        float wv[VEC], bv[VEC];
-        unpack16<DT>(*(const u32x4*)(p.w + (int64_t)c0 * ESZ), wv);
-        unpack16<DT>(*(const u32x4*)(p.b + (int64_t)c0 * ESZ), bv);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = o[e] * wv[e] + bv[e];
-      }
-      u32x4 w;
-      if constexpr (ESZ == 4) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(o[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = pack2<DT>(o[2 * e], o[2 * e + 1]);
-      }
-      *(u32x4*)(yr + (int64_t)c0 * ESZ) = w;
-    }
+    if (c0 < p.cols) ln_store_vec<DT>(p, yr, c0, v[i], mean, rstd);
   }
 }
 
-// Any width or alignment: element loads, the row read three times.
+// Wider aligned rows, one workgroup of NT threads per row: the row held in
+// registers as VPL 16-byte vectors per thread (at most 16 fp32 or 8 16-bit
+// vectors, the most that stay in registers at 4 waves per SIMD), the wave
+// sums combined through LDS in wave order.
+template <int DT, int VPL, int NT>
+__global__ __launch_bounds__(NT) void layer_norm_row_kernel(LnArgs p) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  constexpr int VEC = 16 / ESZ;
+  constexpr int NW = NT / 64;
+  __shared__ float part_s[NW], part_q[NW];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int row = blockIdx.x;  // one row per workgroup: every thread reaches the barriers
+  const char* xr = p.x + (int64_t)row * p.sx * ESZ;
+  float v[VPL][VEC];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)t + NT * i) * VEC;
+    if (c0 < p.cols) {
+      unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v[i]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += v[i][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[i][e] = 0.0f;
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) part_s[wave] = sum;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) total += part_s[w];
+  const float mean = total / (float)p.cols;
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)t + NT * i) * VEC;
+    if (c0 < p.cols) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = v[i][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  sq = wave_sum(sq);
+  if (lane == 0) part_q[wave] = sq;
+  __syncthreads();
+  float totq = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) totq += part_q[w];
+  const float rstd = 1.0f / sqrtf(totq / (float)p.cols + p.eps);
+  char* yr = p.y + (int64_t)row * p.cols * ESZ;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)t + NT * i) * VEC;
+    if (c0 < p.cols) ln_store_vec<DT>(p, yr, c0, v[i], mean, rstd);
+  }
+}
+
+// Rows wider still: 16-byte vectors, the row read three times.
+template <int DT>
+__global__ __launch_bounds__(256) void layer_norm_wide_kernel(LnArgs p) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  constexpr int VEC = 16 / ESZ;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const char* xr = p.x + (int64_t)row * p.sx * ESZ;
+  float sum = 0.0f;
+#pragma unroll 4
+  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+    float v[VEC];
+    unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) sum += v[e];
+  }
+  const float mean = wave_sum(sum) / (float)p.cols;
+  float sq = 0.0f;
+#pragma unroll 4
+  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+    float v[VEC];
+    unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float d = v[e] - mean;
+      sq += d * d;
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)p.cols + p.eps);
+  char* yr = p.y + (int64_t)row * p.cols * ESZ;
+#pragma unroll 4
+  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+    float v[VEC];
+    unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
+    ln_store_vec<DT>(p, yr, c0, v, mean, rstd);
+  }
+}
+
+// Unaligned rows: element loads, the row read three times.
 template <int DT>
 __global__ __launch_bounds__(256) void layer_norm_any_kernel(LnArgs p) {
   constexpr int ESZ = DTraits<DT>::ESZ;
@@ -139,20 +248,38 @@ __global__ __launch_bounds__(256) void layer_norm_any_kernel(LnArgs p) {
   if (row >= p.rows) return;
   const char* xr = p.x + (int64_t)row * p.sx * ESZ;
   float sum = 0.0f;
-  for (int c = lane; c < p.cols; c += 64) sum += load_as_f32<DT>(xr + (int64_t)c * ESZ);
+  for (int64_t c = lane; c < p.cols; c += 64) sum += load_as_f32<DT>(xr + c * ESZ);
   const float mean = wave_sum(sum) / (float)p.cols;
   float sq = 0.0f;
-  for (int c = lane; c < p.cols; c += 64) {
-    const float d = load_as_f32<DT>(xr + (int64_t)c * ESZ) - mean;
+  for (int64_t c = lane; c < p.cols; c += 64) {
+    const float d = load_as_f32<DT>(xr + c * ESZ) - mean;
     sq += d * d;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)p.cols + p.eps);
   char* yr = p.y + (int64_t)row * p.cols * ESZ;
-  for (int c = lane; c < p.cols; c += 64) {
-    float t = (load_as_f32<DT>(xr + (int64_t)c * ESZ) - mean) * rstd;
-    if (p.w != nullptr) t = t * load_as_f32<DT>(p.w + (int64_t)c * ESZ) + load_as_f32<DT>(p.b + (int64_t)c * ESZ);
-    store_from_f32<DT>(yr + (int64_t)c * ESZ, t);
+  for (int64_t c = lane; c < p.cols; c += 64) {
+    float t = (load_as_f32<DT>(xr + c * ESZ) - mean) * rstd;
+    if (p.w != nullptr) t = t * load_as_f32<DT>(p.w + c * ESZ) + load_as_f32<DT>(p.b + c * ESZ);
+    store_from_f32<DT>(yr + c * ESZ, t);
   }
+}
+
+template <int DT, int NT>
+static bool launch_layer_norm_row(const LnArgs& p, hipStream_t stream) {
+  constexpr int VEC = 16 / DTraits<DT>::ESZ;
+  const int64_t per_thread = ((int64_t)p.cols + NT * VEC - 1) / (NT * VEC);
+  const dim3 grid((unsigned)p.rows), block(NT);
+  if (per_thread <= 8) {
+    hipLaunchKernelGGL((layer_norm_row_kernel<DT, 8, NT>), grid, block, 0, stream, p);
+    return true;
+  }
+  if constexpr (DTraits<DT>::ESZ == 4) {
+    if (per_thread <= 16) {
+      hipLaunchKernelGGL((layer_norm_row_kernel<DT, 16, NT>), grid, block, 0, stream, p);
+      return true;
+    }
+  }
+  return false;
 }
 
 template <int DT>
@@ -160,7 +287,11 @@ static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
   constexpr int VEC = 16 / DTraits<DT>::ESZ;
   const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
   const int per_lane = (p.cols + 64 * VEC - 1) / (64 * VEC);
-  if (!vec || per_lane > 16) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
+  if (!vec) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
+  else if (per_lane > 16) {
+    if (!launch_layer_norm_row<DT, 256>(p, stream) && !launch_layer_norm_row<DT, 1024>(p, stream))
+      hipLaunchKernelGGL((layer_norm_wide_kernel<DT>), grid, block, 0, stream, p);
+  }
   else if (per_lane <= 1) hipLaunchKernelGGL((layer_norm_kernel<DT, 1>), grid, block, 0, stream, p);
   else if (per_lane <= 2) hipLaunchKernelGGL((layer_norm_kernel<DT, 2>), grid, block, 0, stream, p);
   else if (per_lane <= 4) hipLaunchKernelGGL((layer_norm_kernel<DT, 4>), grid, block, 0, stream, p);

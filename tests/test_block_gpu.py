@@ -22,7 +22,7 @@ def _say(*parts):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(4096, 768), (8, 512, 768), (7, 100), (3, 5000), (5, 1030), (64, 4096)])
+@pytest.mark.parametrize("shape", [(4096, 768), (8, 512, 768), (7, 100), (3, 5000), (5, 1030), (64, 4096), (6, 16384), (2, 20000), (2, 40000), (1, 140000)])
 def test_layer_norm(gpu, dtype, shape):
     g = torch.Generator().manual_seed(case_seed("ln", shape, dtype))
     x = (torch.randn(*shape, generator=g) * 2 + 0.5).to(dtype)
