@@ -12,7 +12,7 @@
 // fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
 // fp32, rounded once to the output dtype.
 //
-// Attention (fp32, head dim D of 32, 64 or 96): flash-style, four waves per
+// Attention (fp32, head dim D of 32, 64, 96 or 128): flash-style, four waves per
 // 32 query rows, each streaming every fourth 32-key block with an online
 // softmax, their states merged at the end.  A wave computes S^T = K Q^T on
 // v_mfma_f32_32x32x2_f32, so that each lane
@@ -332,13 +332,13 @@ constexpr int kAttnSplit = 4;
 // (rows [32*qb, 32*qb + 32)); with the causal mask it is the pair of blocks t
 // and nqb-1-t, whose key blocks add up to nqb+1 for every t, so all
 // workgroups carry the same work and none waits on the longest rows alone.
-// Two waves per SIMD at every head dim: at dim 96 that spills some
-// registers and is still faster than one wave per SIMD (76 vs 98 us on an
-// 8x12x512 causal problem).
+// Two waves per SIMD up to head dim 96: at 96 that spills some registers and
+// is still faster than one wave per SIMD (76 vs 98 us on an 8x12x512 causal
+// problem).  Head dim 128 holds twice dim 64's fragments: one wave per SIMD.
 template <int D>
-__global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
+__global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(D <= 96 ? 2 : 1, 8)))
 void attention_kernel(AttnArgs p) {
-  static_assert(D % 32 == 0 && D <= 96, "head dim must be 32, 64 or 96");
+  static_assert(D % 32 == 0 && D <= 128, "head dim must be 32, 64, 96 or 128");
   constexpr int NC = D / 8;   // 8-element chunks of the head dim
   constexpr int NB = D / 32;  // 32-row blocks of O^T
   __shared__ float tr[32][D + 1];        // merged output transpose; odd row length: conflict-free column writes
@@ -578,8 +578,8 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
       so == nullptr)
     return set_error(FORGEML_EINVAL, "attention: pointers must be non-NULL");
   if (dtype != FORGEML_DTYPE_F32) return set_error(FORGEML_EINVAL, "attention: only fp32 is built");
-  if (dim != 32 && dim != 64 && dim != 96)
-    return set_error(FORGEML_EINVAL, "attention: head dim must be 32, 64 or 96 (got %lld)", (long long)dim);
+  if (dim != 32 && dim != 64 && dim != 96 && dim != 128)
+    return set_error(FORGEML_EINVAL, "attention: head dim must be 32, 64, 96 or 128 (got %lld)", (long long)dim);
   if (batch <= 0 || heads <= 0 || lq <= 0 || lk <= 0) return set_error(FORGEML_EINVAL, "attention: empty shape");
   if (sq[3] != 1 || sk[3] != 1 || sv[3] != 1)
     return set_error(FORGEML_EINVAL, "attention: q, k and v need a unit stride along the head dim");
@@ -617,7 +617,8 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
   switch (dim) {
     case 32: return launch_attention<32>(p, (hipStream_t)stream);
     case 64: return launch_attention<64>(p, (hipStream_t)stream);
-    default: return launch_attention<96>(p, (hipStream_t)stream);
+    case 96: return launch_attention<96>(p, (hipStream_t)stream);
+    default: return launch_attention<128>(p, (hipStream_t)stream);
   }
 }
 

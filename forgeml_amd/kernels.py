@@ -302,7 +302,7 @@ def matmul(
 # -- the transformer block's other hot ops ----------------------------------------
 
 BLOCK_OPS = ("layer_norm", "sdpa")
-_ATTENTION_DIMS = (32, 64, 96)
+_ATTENTION_DIMS = (32, 64, 96, 128)
 
 
 def _block_op_supported(node, specs) -> bool:

@@ -166,7 +166,7 @@ int forgeml_hip_layer_norm(const void* x, int64_t sx, const void* w, const void*
  * query i see keys j <= i (top-left aligned, as torch's is_causal).  Each of
  * q, k, v, o is described by 4 element strides (batch, head, sequence, dim);
  * q, k and v need unit stride along dim and 16-byte aligned rows of q and k.
- * dim is 32, 64 or 96.  Replaces F.scaled_dot_product_attention of the
+ * dim is 32, 64, 96 or 128.  Replaces F.scaled_dot_product_attention of the
  * `sdpa` op without an attention mask (src/forgeml/ops.py, _sdpa).
  */
 int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk,

@@ -54,7 +54,8 @@ def _attention_inputs(b, h, lq, lk, d, seed):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("b,h,lq,lk,d", [(2, 3, 100, 100, 64), (1, 2, 33, 33, 32), (2, 2, 64, 64, 96),
-                                          (1, 4, 512, 512, 64), (2, 1, 40, 70, 64), (1, 1, 1, 1, 64)])
+                                          (1, 4, 512, 512, 64), (2, 1, 40, 70, 64), (1, 1, 1, 1, 64),
+                                          (2, 3, 100, 100, 128), (1, 2, 300, 300, 128)])
 def test_attention(gpu, causal, b, h, lq, lk, d):
     seed = case_seed("attn", b, h, lq, lk, d, causal)
     q, k, v = _attention_inputs(b, h, lq, lk, d, seed)
