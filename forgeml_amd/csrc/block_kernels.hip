@@ -282,8 +282,12 @@ static bool launch_layer_norm_row(const LnArgs& p, hipStream_t stream) {
   return false;
 }
 
+// Rows per launch: a dispatch covers fewer than 2^32 work-items, and a
+// workgroup-per-row kernel has 1024 threads per row at most.
+static constexpr int64_t kLnRowsPerLaunch = (int64_t)1 << 21;
+
 template <int DT>
-static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
+static void launch_layer_norm_chunk(const LnArgs& p, bool vec, hipStream_t stream) {
   constexpr int VEC = 16 / DTraits<DT>::ESZ;
   const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
   const int per_lane = (p.cols + 64 * VEC - 1) / (64 * VEC);
@@ -297,8 +301,20 @@ static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
   else if (per_lane <= 4) hipLaunchKernelGGL((layer_norm_kernel<DT, 4>), grid, block, 0, stream, p);
   else if (per_lane <= 8) hipLaunchKernelGGL((layer_norm_kernel<DT, 8>), grid, block, 0, stream, p);
   else hipLaunchKernelGGL((layer_norm_kernel<DT, 16>), grid, block, 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return set_error(FORGEML_EHIP, "layer_norm launch failed: %s", hipGetErrorString(e));
+}
+
+template <int DT>
+static int launch_layer_norm(const LnArgs& p, bool vec, hipStream_t stream) {
+  constexpr int ESZ = DTraits<DT>::ESZ;
+  for (int64_t r0 = 0; r0 < p.rows; r0 += kLnRowsPerLaunch) {
+    LnArgs c = p;
+    c.x = p.x + r0 * p.sx * ESZ;
+    c.y = p.y + r0 * p.cols * ESZ;
+    c.rows = (int)(p.rows - r0 < kLnRowsPerLaunch ? p.rows - r0 : kLnRowsPerLaunch);
+    launch_layer_norm_chunk<DT>(c, vec, stream);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(FORGEML_EHIP, "layer_norm launch failed: %s", hipGetErrorString(e));
+  }
   return FORGEML_OK;
 }
 
@@ -593,7 +609,9 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
       ((lk - 1) * sv[2] + dim) * 4 >= ((int64_t)1 << 31))
     return set_error(FORGEML_EINVAL, "attention: a (batch, head) slice exceeds 2 GiB");
   const int64_t nqb = (lq + 31) / 32;
-  if (batch * heads * nqb > INT_MAX) return set_error(FORGEML_EINVAL, "attention: too many query blocks");
+  // One workgroup per work item: the dispatch must cover fewer than 2^32 work-items.
+  if (batch * heads * nqb * (kAttnSplit * 64) >= ((int64_t)1 << 32))
+    return set_error(FORGEML_EINVAL, "attention: more than 2^24 query blocks in one call");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(FORGEML_EINVAL, "attention: scale must be finite and positive");
   AttnArgs p;
   p.q = (const float*)q;

@@ -105,6 +105,14 @@ static bool needs_small_tile(int ma, int mb) {
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Work-items of one launch of tile t (a dispatch covers fewer than 2^32);
+// the few-row kernel is bounded by one workgroup per 16 columns and 16 rows.
+static constexpr int64_t kMaxItems = (int64_t)1 << 32;
+static int64_t launch_items(const TileConfig& t, int64_t m, int64_t n, int64_t splits) {
+  const int64_t wgs = t.kind == KIND_SKINNY ? cdiv(n, 16) * cdiv(m, 16) : cdiv(m, t.bm) * cdiv(n, t.bn) * splits;
+  return wgs * (t.wm * t.wn * 64);
+}
+
 // Load width (bytes) of the few-row kernel for these operands, or 0 when it
 // cannot run them: it needs M <= 64, both operands K-contiguous, and 32-bit
 // byte offsets over A and over 16 rows of B.
@@ -332,7 +340,9 @@ static int plan_launch(const void* a, int64_t sam, int64_t sak, const void* b, i
   const int mb = operand_mode(b, n, sbn, sbk, k, esz);
   const int lw = skinny_width(m, k, sam, sak, sbn, sbk, ma, mb, esz);
   if (config_id == FORGEML_CONFIG_AUTO)
-    config_id = skinny_preferred(m, n, k, lw, esz) ? skinny_id(dclass_of(dtype)) : select_config(m, n, k, dtype, ma, mb);
+    config_id = skinny_preferred(m, n, k, lw, esz) && launch_items(kTiles[skinny_id(dclass_of(dtype))], m, n, 1) < kMaxItems
+                    ? skinny_id(dclass_of(dtype))
+                    : select_config(m, n, k, dtype, ma, mb);
   const TileConfig& t = kTiles[config_id];
   if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
     return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
@@ -347,8 +357,8 @@ static int plan_launch(const void* a, int64_t sam, int64_t sak, const void* b, i
   out.sak = sak;
   out.sbk = sbk;
   out.sbn = sbn;
-  if (cdiv(m, t.bm) * cdiv(n, t.bn) * out.split.splits > INT_MAX)
-    return set_error(FORGEML_EINVAL, "too many output tiles");
+  if (launch_items(t, m, n, out.split.splits) >= kMaxItems)
+    return set_error(FORGEML_EINVAL, "shape needs 2^32 or more work-items in one launch with config %d", config_id);
   return FORGEML_OK;
 }
 

@@ -117,16 +117,17 @@ def test_tiled_fp32_m_contiguous_a_beyond_2gib(gpu):
 
 
 def test_layer_norm_beyond_4gib(gpu):
-    rows, cols = (1 << 20) + 3, 1024
+    """8.6 GB in and out; 2^21 + 3 rows, so the rows take two launches."""
+    rows, cols = (1 << 21) + 3, 1024
     seed = case_seed("large-ln", rows, cols)
     _say("large layer_norm fp32", rows, cols, seed)
     x = _randn((rows, cols), seed, gpu, 2.0, torch.float32)
     w = _randn((cols,), seed + 1, gpu, 1.0, torch.float32)
     b = _randn((cols,), seed + 2, gpu, 0.1, torch.float32)
-    assert x.numel() * 4 > 4 * GIB
+    assert x.numel() * 4 > 8 * GIB
     y = kernels.layer_norm(x, (cols,), w, b, 1e-5)
     torch.cuda.synchronize()
-    r = _around(0, (2 * GIB) // (cols * 4), (4 * GIB) // (cols * 4), rows - 1, hi=rows).to(gpu)
+    r = _around(0, (2 * GIB) // (cols * 4), (4 * GIB) // (cols * 4), 1 << 21, rows - 1, hi=rows).to(gpu)
     expected = F.layer_norm(x[r].cpu(), (cols,), w.cpu(), b.cpu(), 1e-5)
     torch.testing.assert_close(y[r].cpu(), expected, rtol=1e-4, atol=1e-5)
     del x, w, b, y

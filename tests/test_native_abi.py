@@ -191,3 +191,37 @@ def test_block_kernel_argument_errors():
     bad = (ctypes.c_int64 * 4)(4096, 64 * 64, 64, 2)
     assert lib.forgeml_hip_attention(dummy, bad, dummy, st, dummy, st, dummy, st, 1, 1, 64, 64, 64, 1, 0.125, f32,
                                      None) == _native.EINVAL
+
+
+def test_launch_size_limits():
+    """A dispatch covers fewer than 2^32 work-items: shapes past that are
+    refused with the config asked for, and AUTO plans a config that fits
+    (host-side planning only: nothing is launched)."""
+    lib = _native.load()
+    out = (ctypes.c_int64 * 4)()
+
+    def plan(m, n, k, ld, dtype, cid):
+        rc = lib.forgeml_hip_gemm_plan(ctypes.c_void_p(1 << 40), ld, 1, ctypes.c_void_p(1 << 41), 1, ld, m, n, k,
+                                       dtype, cid, out)
+        return rc, tuple(out)
+
+    f32, bf16 = _native.DTYPE_F32, _native.DTYPE_BF16
+    tile64 = kernels.config_id(kernels.candidates(torch.float32)[1], torch.float32)
+    # 2^18 x 2^18 outputs: 2^24 workgroups of 256 threads on the 64x64 tile.
+    assert plan(1 << 18, 1 << 18, 64, 64, f32, tile64)[0] == _native.EINVAL
+    assert "work-items" in _native.last_error()
+    rc, (cid, _, _, _) = plan(1 << 18, 1 << 18, 64, 64, f32, -1)
+    assert rc == _native.OK and kernels.CANDIDATES[cid].block_m >= 128
+    # 2^27 columns on the few-row kernel: 2^23 workgroups of 512 threads.
+    few_row = kernels.config_id(kernels.SKINNY_H16, torch.bfloat16)
+    assert plan(16, 1 << 27, 16, 16, bf16, few_row)[0] == _native.EINVAL
+    rc, (_, _, _, kind) = plan(16, 1 << 27, 16, 16, bf16, -1)
+    assert rc == _native.OK and kind == 0
+    rc, (_, _, _, kind) = plan(16, 1 << 25, 16, 16, bf16, few_row)
+    assert rc == _native.OK and kind == 1
+    # Attention: one 256-thread workgroup per query block.
+    dummy = ctypes.c_void_p(256)
+    st = (ctypes.c_int64 * 4)(1 << 20, 512 * 32, 32, 1)
+    args = (dummy, st, dummy, st, dummy, st, dummy, st)
+    assert lib.forgeml_hip_attention(*args, 1 << 20, 16, 512, 512, 32, 0, 0.125, f32, None) == _native.EINVAL
+    assert "query blocks" in _native.last_error()
