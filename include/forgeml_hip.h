@@ -78,8 +78,10 @@ extern "C" {
  *            (may be NULL/0 when forgeml_hip_gemm_workspace_size is 0)
  *   stream   hipStream_t to launch on (NULL = the null stream)
  *
- * Returns FORGEML_OK or a negative FORGEML_E* code.  The launch is
- * asynchronous; errors raised while the kernel runs surface on the stream.
+ * Returns FORGEML_OK or a negative FORGEML_E* code (FORGEML_EINVAL also when
+ * the config's grid would need 2^32 or more work-items; FORGEML_CONFIG_AUTO
+ * plans a config that fits).  The launch is asynchronous; errors raised
+ * while the kernel runs surface on the stream.
  */
 int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
                      const void* b, int64_t sbk, int64_t sbn,
