@@ -279,6 +279,47 @@ def _measured_traffic(key: str):
     return None if entry is None else entry["traffic_bytes"]
 
 
+LN_SHAPES = [(4096, 768, torch.float32), (4096, 4096, torch.float32), (4096, 8192, torch.float32),
+             (2048, 12288, torch.bfloat16), (4096, 16384, torch.bfloat16), (1024, 65536, torch.float32),
+             (512, 200000, torch.float32)]
+ATTN_CASES = [(8, 12, 512, 64, True), (8, 12, 512, 128, True), (4, 32, 1024, 128, True), (4, 32, 1024, 128, False)]
+
+
+def block_op_workloads(steps: int, warmup: int):
+    """The transformer block's LayerNorm and attention kernels against torch's
+    GPU kernels for the same ops, per-launch HIP-event µs (median), one record
+    per case.  LayerNorm also reports its HBM floor (read x, write y at 8 TB/s)."""
+    import torch.nn.functional as F
+
+    from forgeml_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def med_us(fn):
+        _, per = _time_launches(fn, steps, warmup)
+        return round(statistics.median(per) * 1e3, 2)
+
+    for rows, cols, dt in LN_SHAPES:
+        x = torch.randn(rows, cols, device=dev, generator=g).to(dt)
+        w = torch.randn(cols, device=dev, generator=g).to(dt)
+        b = torch.randn(cols, device=dev, generator=g).to(dt)
+        ours = med_us(lambda: kernels.layer_norm(x, (cols,), w, b, 1e-5))
+        ref = med_us(lambda: F.layer_norm(x, (cols,), w, b, 1e-5))
+        floor = 2 * x.numel() * x.element_size() / (HBM_GBPS * 1e3)
+        yield {"workload": f"layer_norm_{DTYPE_NAMES[dt]}_{rows}x{cols}", "us": ours, "torch_gpu_us": ref,
+               "hbm_floor_us": round(floor, 2), "hbm_frac": round(floor / ours, 3)}
+        del x, w, b
+    for bsz, heads, seq, dim, causal in ATTN_CASES:
+        q, k, v = (torch.randn(bsz, heads, seq, dim, device=dev, generator=g) for _ in range(3))
+        ours = med_us(lambda: kernels.attention(q, k, v, is_causal=causal))
+        ref = med_us(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal))
+        flop = 4 * bsz * heads * seq * seq * dim * (0.5 if causal else 1.0)
+        yield {"workload": f"attention_fp32_{bsz}x{heads}x{seq}x{dim}_{'causal' if causal else 'full'}", "us": ours,
+               "torch_gpu_us": ref, "tflops": round(flop / ours / 1e6, 1)}
+        del q, k, v
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +333,8 @@ def main() -> int:
                     help="with --only: force this tile configuration instead of the shape heuristic")
     ap.add_argument("--vendor", action="store_true",
                     help="with --only: time torch's library GEMM (hipBLASLt) on the same operands instead")
+    ap.add_argument("--block-ops", action="store_true",
+                    help="time the LayerNorm and attention kernels against torch's GPU kernels instead")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -303,6 +346,10 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.block_ops:
+        for rec in block_op_workloads(args.steps, args.warmup):
+            print(json.dumps(rec), flush=True)
+        return 0
     if args.only:
         config = None
         if args.tile:

@@ -7,7 +7,8 @@
 //
 // LayerNorm: one wave per row; the row is held in registers as 16-byte
 // vectors (up to 16 per lane; wider aligned rows spread over a workgroup of
-// 256 or 1024 threads, and past that are read three times as vectors), mean
+// 256 or 1024 threads, and past that are read three times as vectors by a
+// 1024-thread workgroup per row), mean
 // and variance are two passes over those registers with reductions in a
 // fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
 // fp32, rounded once to the output dtype.
@@ -200,27 +201,36 @@ __global__ __launch_bounds__(NT) void layer_norm_row_kernel(LnArgs p) {
   }
 }
 
-// Rows wider still: 16-byte vectors, the row read three times.
+// Rows wider still: one workgroup of 1024 threads per row, 16-byte vectors,
+// the row read three times (the re-reads mostly from cache).
+constexpr int kLnWideThreads = 1024;
 template <int DT>
-__global__ __launch_bounds__(256) void layer_norm_wide_kernel(LnArgs p) {
+__global__ __launch_bounds__(kLnWideThreads) void layer_norm_wide_kernel(LnArgs p) {
   constexpr int ESZ = DTraits<DT>::ESZ;
   constexpr int VEC = 16 / ESZ;
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= p.rows) return;
+  constexpr int NT = kLnWideThreads, NW = NT / 64;
+  __shared__ float part_s[NW], part_q[NW];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int row = blockIdx.x;  // one row per workgroup: every thread reaches the barriers
   const char* xr = p.x + (int64_t)row * p.sx * ESZ;
   float sum = 0.0f;
 #pragma unroll 4
-  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
     float v[VEC];
     unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) sum += v[e];
   }
-  const float mean = wave_sum(sum) / (float)p.cols;
+  sum = wave_sum(sum);
+  if (lane == 0) part_s[wave] = sum;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) total += part_s[w];
+  const float mean = total / (float)p.cols;
   float sq = 0.0f;
 #pragma unroll 4
-  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
     float v[VEC];
     unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
 #pragma unroll
@@ -229,10 +239,16 @@ __global__ __launch_bounds__(256) void layer_norm_wide_kernel(LnArgs p) {
       sq += d * d;
     }
   }
-  const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)p.cols + p.eps);
+  sq = wave_sum(sq);
+  if (lane == 0) part_q[wave] = sq;
+  __syncthreads();
+  float totq = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) totq += part_q[w];
+  const float rstd = 1.0f / sqrtf(totq / (float)p.cols + p.eps);
   char* yr = p.y + (int64_t)row * p.cols * ESZ;
 #pragma unroll 4
-  for (int64_t c0 = lane * VEC; c0 < p.cols; c0 += 64 * VEC) {
+  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
     float v[VEC];
     unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
     ln_store_vec<DT>(p, yr, c0, v, mean, rstd);
@@ -294,7 +310,7 @@ static void launch_layer_norm_chunk(const LnArgs& p, bool vec, hipStream_t strea
   if (!vec) hipLaunchKernelGGL((layer_norm_any_kernel<DT>), grid, block, 0, stream, p);
   else if (per_lane > 16) {
     if (!launch_layer_norm_row<DT, 256>(p, stream) && !launch_layer_norm_row<DT, 1024>(p, stream))
-      hipLaunchKernelGGL((layer_norm_wide_kernel<DT>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((layer_norm_wide_kernel<DT>), dim3((unsigned)p.rows), dim3(kLnWideThreads), 0, stream, p);
   }
   else if (per_lane <= 1) hipLaunchKernelGGL((layer_norm_kernel<DT, 1>), grid, block, 0, stream, p);
   else if (per_lane <= 2) hipLaunchKernelGGL((layer_norm_kernel<DT, 2>), grid, block, 0, stream, p);
