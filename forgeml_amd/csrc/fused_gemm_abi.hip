@@ -278,7 +278,9 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
 int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype) {
   if (dtype < FORGEML_DTYPE_F32 || dtype > FORGEML_DTYPE_F16) return set_error(FORGEML_EINVAL, "unknown dtype %d", dtype);
   if (m <= 0 || n <= 0 || k <= 0) return set_error(FORGEML_EINVAL, "select_config: M, N, K must be positive");
-  if (m <= kSkinnyMaxRows && skinny_preferred(m, n, k, 16, esize_of(dtype))) return skinny_id(dclass_of(dtype));
+  if (m <= kSkinnyMaxRows && skinny_preferred(m, n, k, 16, esize_of(dtype)) &&
+      launch_items(kTiles[skinny_id(dclass_of(dtype))], m, n, 1) < kMaxItems)
+    return skinny_id(dclass_of(dtype));
   return select_config(m, n, k, dtype, MODE_K, MODE_K);
 }
 

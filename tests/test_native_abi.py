@@ -215,8 +215,9 @@ def test_launch_size_limits():
     # 2^27 columns on the few-row kernel: 2^23 workgroups of 512 threads.
     few_row = kernels.config_id(kernels.SKINNY_H16, torch.bfloat16)
     assert plan(16, 1 << 27, 16, 16, bf16, few_row)[0] == _native.EINVAL
-    rc, (_, _, _, kind) = plan(16, 1 << 27, 16, 16, bf16, -1)
+    rc, (cid, _, _, kind) = plan(16, 1 << 27, 16, 16, bf16, -1)
     assert rc == _native.OK and kind == 0
+    assert lib.forgeml_hip_select_config(16, 1 << 27, 16, bf16) == cid
     rc, (_, _, _, kind) = plan(16, 1 << 25, 16, 16, bf16, few_row)
     assert rc == _native.OK and kind == 1
     # Attention: one 256-thread workgroup per query block.
