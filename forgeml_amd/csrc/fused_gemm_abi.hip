@@ -210,6 +210,8 @@ static double tile_cost(const TileConfig& t, int64_t m, int64_t n, int64_t k, in
 // does not fit the transposing loaders); layouts whose kernels exist only
 // for small tiles choose among those, and 16-bit element loads (whose staged
 // values and addresses outgrow the registers of larger tiles) use 64x64.
+// Tiles whose grid would reach 2^32 work-items are skipped; -1 when no
+// allowed tile fits.
 static int select_config(int64_t m, int64_t n, int64_t k, int dtype, int ma, int mb) {
   const int dclass = dclass_of(dtype);
   const int esz = esize_of(dtype);
@@ -225,6 +227,7 @@ static int select_config(int64_t m, int64_t n, int64_t k, int dtype, int ma, int
     if (t.wm * t.wn > 4 && dclass == 1 && !all_k) continue;
     const int64_t area = (int64_t)t.bm * t.bn;
     if (area > max_area) continue;
+    if (launch_items(t, m, n, split_plan(t, m, n, k, esz).splits) >= kMaxItems) continue;
     const double cost = tile_cost(t, m, n, k, esz);
     bool take = best < 0 || cost < best_cost * 0.99;  // clearly cheaper
     if (!take && cost <= best_cost * 1.01) take = area > (int64_t)kTiles[best].bm * kTiles[best].bn;  // a tie: bigger
@@ -281,7 +284,9 @@ int forgeml_hip_select_config(int64_t m, int64_t n, int64_t k, int32_t dtype) {
   if (m <= kSkinnyMaxRows && skinny_preferred(m, n, k, 16, esize_of(dtype)) &&
       launch_items(kTiles[skinny_id(dclass_of(dtype))], m, n, 1) < kMaxItems)
     return skinny_id(dclass_of(dtype));
-  return select_config(m, n, k, dtype, MODE_K, MODE_K);
+  const int id = select_config(m, n, k, dtype, MODE_K, MODE_K);
+  if (id < 0) return set_error(FORGEML_EINVAL, "select_config: no tile fits a launch of fewer than 2^32 work-items");
+  return id;
 }
 
 int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t dtype, int32_t config_id) {
@@ -298,6 +303,7 @@ int64_t forgeml_hip_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int32_t
   int64_t most = 0;
   for (const auto& mp : kModePairs) {
     const int id = select_config(m, n, k, dtype, mp[0], mp[1]);
+    if (id < 0) continue;
     most = std::max(most, workspace_bytes_for(split_plan(kTiles[id], m, n, k, esz), m, n));
   }
   return most;
@@ -345,6 +351,8 @@ static int plan_launch(const void* a, int64_t sam, int64_t sak, const void* b, i
     config_id = skinny_preferred(m, n, k, lw, esz) && launch_items(kTiles[skinny_id(dclass_of(dtype))], m, n, 1) < kMaxItems
                     ? skinny_id(dclass_of(dtype))
                     : select_config(m, n, k, dtype, ma, mb);
+  if (config_id < 0)
+    return set_error(FORGEML_EINVAL, "shape needs 2^32 or more work-items in one launch with every tile this layout allows");
   const TileConfig& t = kTiles[config_id];
   if (t.dclass != dclass_of(dtype) || t.launch[dtype] == nullptr)
     return set_error(FORGEML_ECONFIG, "config %d is not built for dtype %d", config_id, dtype);
@@ -353,6 +361,12 @@ static int plan_launch(const void* a, int64_t sam, int64_t sak, const void* b, i
                      kSkinnyMaxRows);
   out.config_id = config_id;
   out.combo = t.kind == KIND_SKINNY ? lw : combo_of(ma, mb, (int64_t)t.bm * t.bn <= kSmallTileArea);
+  if (t.kind == KIND_TILED && !combo_supported(t.dclass, t.bm, t.bn, t.wm * t.wn, out.combo))
+    return set_error(FORGEML_ECONFIG,
+                     "config %d (%dx%d, %d waves) is not built for this operand layout (%s); choose a smaller tile "
+                     "or FORGEML_CONFIG_AUTO",
+                     config_id, t.bm, t.bn, t.wm * t.wn,
+                     t.wm * t.wn > 4 ? "it takes K-contiguous A and B with 16-byte rows" : "16-bit element loads");
   out.split = split_plan(t, m, n, k, esz);
   out.ws_need = workspace_bytes_for(out.split, m, n);
   out.sam = sam;

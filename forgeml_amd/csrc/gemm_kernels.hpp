@@ -164,21 +164,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// Cheaper forms for 16-bit outputs, whose rounding (2^-9 relative for bf16)
-// is far coarser than their error.
-//  * erf GELU = x * Phi(x), with Phi(-|x|) = erfc(|x|/sqrt 2)/2 from
-//    Abramowitz & Stegun 7.1.26: erfc(z) = t(a1 + t(a2 + t(a3 + t(a4 + t a5))))
-//    exp(-z^2), t = 1/(1 + p z), |error| <= 1.5e-7.
+// Cheaper forms for 16-bit outputs, accurate to a few fp32 ulps relative to
+// the result everywhere, far inside the output rounding (2^-9 relative for
+// bf16, 2^-11 for fp16).
+//  * erf GELU = x * Phi(x), with Phi(-|x|) = erfc(|x|/sqrt 2)/2 from the
+//    Chebyshev fit of Press et al., Numerical Recipes in C (2nd ed.), 6.2
+//    ("erfcc"): erfc(z) = t exp(-z^2 + P(t)), t = 1/(1 + z/2), P a degree-9
+//    polynomial, relative error below 1.2e-7 for every z >= 0.  A relative
+//    bound matters in the negative tail, where x Phi(x) is small: an
+//    absolute-error fit (Abramowitz & Stegun 7.1.26) is off there by up to
+//    4 % of the result.
 //  * tanh GELU = x * sigmoid(2u) = x / (1 + exp(-2u)), an identity of the
-//    tanh form.
+//    tanh form that avoids 1 + tanh(u) cancelling for negative x.
 __device__ __forceinline__ float gelu_erf_16(float x) {
   const float z = fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  const float q = 0.5f * poly * t * __expf(-z * z);  // Phi(-|x|)
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = fmaf(0.17087277f, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  const float q = 0.5f * t * __expf(fmaf(-z, z, p));  // Phi(-|x|)
   return x * (x >= 0.0f ? 1.0f - q : q);
 }
 __device__ __forceinline__ float gelu_tanh_16(float x) {

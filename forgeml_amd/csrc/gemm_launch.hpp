@@ -26,6 +26,18 @@ enum : int {
 
 constexpr int kSmallTileArea = 128 * 128;
 
+// Whether a tile is built for an operand combination.  16-bit element loads
+// (COMBO_G_*) stage 32 packed values per thread, and tiles above 64x64 then
+// run out of registers beside their accumulators and spill to scratch; the
+// 8-wave 16-bit tile's budget fits only the DMA loaders of two K-contiguous
+// operands.  Those pairs are not built, and the planner refuses a request
+// for one; the shape heuristic never chooses them.
+constexpr bool combo_supported(int dclass, int bm, int bn, int waves, int combo) {
+  if (dclass == 1 && waves > 4 && combo != COMBO_K_K) return false;
+  if (dclass == 1 && bm * bn > 64 * 64 && (combo == COMBO_G_G || combo == COMBO_G_MN)) return false;
+  return true;
+}
+
 // Sets the thread-local error text; returns `code`.
 int set_error(int code, const char* fmt, ...);
 
@@ -85,22 +97,32 @@ int launch_one(const GemmArgs& p, hipStream_t stream) {
   return p.splits > 1 ? launch_reduce<DT>(p, stream) : 0;
 }
 
+// One combination of a tile, or an error when the tile is not built for it
+// (the planner refuses those requests first).
+template <int DT, int BM, int BN, int WM, int WN, int COMBO, int AMODE, int BMODE>
+int launch_combo(const GemmArgs& p, hipStream_t stream) {
+  if constexpr (combo_supported(DT == DT_F32 ? 0 : 1, BM, BN, WM * WN, COMBO))
+    return launch_one<DT, BM, BN, WM, WN, AMODE, BMODE>(p, stream);
+  else
+    return set_error(-2, "tile %dx%d (%d waves) is not built for operand combination %d", BM, BN, WM * WN, COMBO);
+}
+
 template <int DT, int BM, int BN, int WM, int WN>
 int launch_tile(const GemmArgs& p, int combo, hipStream_t stream) {
   if constexpr (BM * BN <= kSmallTileArea) {
     switch (combo) {
-      case COMBO_K4_K4: return launch_one<DT, BM, BN, WM, WN, MODE_K4, MODE_K4>(p, stream);
-      case COMBO_K4_MN: return launch_one<DT, BM, BN, WM, WN, MODE_K4, MODE_MN>(p, stream);
-      case COMBO_G_MN: return launch_one<DT, BM, BN, WM, WN, MODE_G, MODE_MN>(p, stream);
+      case COMBO_K4_K4: return launch_combo<DT, BM, BN, WM, WN, COMBO_K4_K4, MODE_K4, MODE_K4>(p, stream);
+      case COMBO_K4_MN: return launch_combo<DT, BM, BN, WM, WN, COMBO_K4_MN, MODE_K4, MODE_MN>(p, stream);
+      case COMBO_G_MN: return launch_combo<DT, BM, BN, WM, WN, COMBO_G_MN, MODE_G, MODE_MN>(p, stream);
       default: break;
     }
   }
   switch (combo) {
-    case COMBO_K_K: return launch_one<DT, BM, BN, WM, WN, MODE_K, MODE_K>(p, stream);
-    case COMBO_K_MN: return launch_one<DT, BM, BN, WM, WN, MODE_K, MODE_MN>(p, stream);
-    case COMBO_MN_K: return launch_one<DT, BM, BN, WM, WN, MODE_MN, MODE_K>(p, stream);
-    case COMBO_MN_MN: return launch_one<DT, BM, BN, WM, WN, MODE_MN, MODE_MN>(p, stream);
-    default: return launch_one<DT, BM, BN, WM, WN, MODE_G, MODE_G>(p, stream);
+    case COMBO_K_K: return launch_combo<DT, BM, BN, WM, WN, COMBO_K_K, MODE_K, MODE_K>(p, stream);
+    case COMBO_K_MN: return launch_combo<DT, BM, BN, WM, WN, COMBO_K_MN, MODE_K, MODE_MN>(p, stream);
+    case COMBO_MN_K: return launch_combo<DT, BM, BN, WM, WN, COMBO_MN_K, MODE_MN, MODE_K>(p, stream);
+    case COMBO_MN_MN: return launch_combo<DT, BM, BN, WM, WN, COMBO_MN_MN, MODE_MN, MODE_MN>(p, stream);
+    default: return launch_combo<DT, BM, BN, WM, WN, COMBO_G_G, MODE_G, MODE_G>(p, stream);
   }
 }
 

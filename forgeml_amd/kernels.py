@@ -364,7 +364,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, is_causal: b
     qkv = []
     for t in (q, k, v):
         if t.stride(3) != 1 or t.data_ptr() % 16 or any(s % 4 for s in t.stride()[:3]):
-            t = t.contiguous()
+            # A fresh allocation: contiguous() would hand back a contiguous
+            # tensor whose storage offset leaves it misaligned.
+            t = t.clone(memory_format=torch.contiguous_format)
         qkv.append(t)
     out = torch.empty(bsz, lq, heads, dim, dtype=q.dtype, device=q.device).transpose(1, 2)
     strides = [(ctypes.c_int64 * 4)(*t.stride()) for t in (*qkv, out)]

@@ -80,7 +80,8 @@ extern "C" {
  *
  * Returns FORGEML_OK or a negative FORGEML_E* code (FORGEML_EINVAL also when
  * the config's grid would need 2^32 or more work-items; FORGEML_CONFIG_AUTO
- * plans a config that fits).  The launch is asynchronous; errors raised
+ * plans a config that fits when the operands' layout allows one).  The
+ * launch is asynchronous; errors raised
  * while the kernel runs surface on the stream.
  */
 int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,

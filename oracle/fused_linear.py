@@ -69,6 +69,131 @@ def kernel_contract(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None 
     return v32.to(dtype)
 
 
+# -- ulp-level check of 16-bit outputs against the epilogue contract -------------
+
+_MANT_BITS = {torch.bfloat16: 7, torch.float16: 10}
+
+
+def ulp_index(x: torch.Tensor) -> torch.Tensor:
+    """16-bit float bit patterns mapped to integers monotone in the value
+    (+0 and -0 both 0), so that a difference of ordered values counts ulps."""
+    bits = x.contiguous().view(torch.int16).to(torch.int64) & 0xFFFF
+    mag = bits & 0x7FFF
+    return torch.where(bits >= 0x8000, -mag, mag)
+
+
+def from_ulp_index(o: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    bits = torch.where(o < 0, (-o) | 0x8000, o)
+    bits = torch.where(bits >= 0x8000, bits - 0x10000, bits)
+    return bits.to(torch.int16).view(dtype)
+
+
+def gelu_f64(x: torch.Tensor, approximate: str = "none") -> torch.Tensor:
+    """GELU in fp64 without cancellation for negative x: x/2 erfc(-x/sqrt 2)
+    (erf form) and x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3) (tanh form,
+    the identity 0.5 (1 + tanh u) = sigmoid(2u))."""
+    x = x.to(torch.float64)
+    if approximate == "tanh":
+        u = math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)
+        return x * torch.sigmoid(2.0 * u)
+    return 0.5 * x * torch.special.erfc(-x / math.sqrt(2.0))
+
+
+def _epilogue_f64(v: torch.Tensor, bias: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor:
+    """rnd(v + bias) in fp64 for v already in ``dtype`` (src/forgeml/_triton.py:43-46)."""
+    x = v.to(torch.float64)
+    if bias is not None:
+        x = (x + bias.detach().cpu().to(torch.float64)).to(dtype).to(torch.float64)
+    return x
+
+
+def _activate_f64(x: torch.Tensor, activation: str, approximate: str) -> torch.Tensor:
+    if activation == "gelu":
+        return gelu_f64(x, approximate)
+    if activation == "relu":
+        return torch.clamp_min(x, 0)
+    return x
+
+
+def _gelu_argmin(approximate: str) -> float:
+    """Where GELU takes its minimum (near -0.75), by ternary search in fp64."""
+    lo, hi = -1.5, 0.0
+    f = lambda t: float(gelu_f64(torch.tensor([t], dtype=torch.float64), approximate))  # noqa: E731
+    for _ in range(200):
+        m1, m2 = lo + (hi - lo) / 3, hi - (hi - lo) / 3
+        if f(m1) < f(m2):
+            hi = m2
+        else:
+            lo = m1
+    return 0.5 * (lo + hi)
+
+
+_GELU_ARGMIN = {approx: _gelu_argmin(approx) for approx in ("none", "tanh")}
+
+
+def contract_ulp_check(got: torch.Tensor, a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = None,
+                       activation: str = "none", approximate: str = "none",
+                       acc: torch.Tensor | None = None) -> dict:
+    """Ulp-level check of a 16-bit kernel output against the epilogue contract.
+
+    The contract is C = act(rnd(rnd(sum A B) + bias)) (src/forgeml/_triton.py:
+    43-57).  The kernel sums the exact products in fp32 in its own order, so
+    its sum lies within E = gamma_K sum |A||B| of the exact one (gamma_K =
+    K u / (1 - K u), u = 2^-24: the bound for any summation order).  Each
+    element's sum is therefore known to an interval [S - E, S + E]; rnd, the
+    bias add and the next rnd are monotone, so the pre-activation lies in
+    [x_lo, x_hi], and the output must lie within one ulp of act over that
+    range (the activation evaluated exactly; GELU's minimum near -0.75 is
+    included when the range spans it), or within the dtype's smallest
+    normal of it, for results the fp32 arithmetic flushes.  Where the sum
+    does not cancel, E is under about one ulp, so the range is one or two
+    values wide.
+
+    Reported: ``bad`` (elements outside), ``exact_frac`` (elements equal to
+    act(rnd(rnd(S) + bias)) from the exact sum S) and ``max_ulp`` (the
+    largest distance outside the range).  A test requires bad == 0 and
+    exact_frac >= 0.99: a wrong activation form, a skipped rounding step or
+    a truncating conversion moves far more than 1 % of the elements.
+    ``acc``: the fp64 sum S, when the caller already has it.
+    """
+    dtype = got.dtype
+    if dtype not in _MANT_BITS:
+        raise ValueError(f"contract_ulp_check is for 16-bit outputs, got {dtype}")
+    got = got.detach().cpu()
+    a64 = a.detach().cpu().to(torch.float64)
+    b64 = b.detach().cpu().to(torch.float64)
+    if acc is None:
+        acc = a64 @ b64
+    k = a64.shape[1]
+    u = 2.0 ** -24
+    err = (k * u / (1 - k * u)) * (a64.abs() @ b64.abs())
+    x_lo = _epilogue_f64((acc - err).to(dtype), bias, dtype)
+    x_hi = _epilogue_f64((acc + err).to(dtype), bias, dtype)
+    y_lo = _activate_f64(x_lo, activation, approximate)
+    y_hi = _activate_f64(x_hi, activation, approximate)
+    low, high = torch.minimum(y_lo, y_hi), torch.maximum(y_lo, y_hi)
+    if activation == "gelu":
+        t = _GELU_ARGMIN[approximate]
+        spans = (x_lo <= t) & (t <= x_hi)
+        low = torch.where(spans, torch.minimum(low, gelu_f64(torch.tensor(t, dtype=torch.float64), approximate)), low)
+    low, high = low.to(dtype), high.to(dtype)
+    og = ulp_index(got)
+    below = (ulp_index(low) - og).clamp_min(0)
+    above = (og - ulp_index(high)).clamp_min(0)
+    outside = torch.maximum(below, above)
+    tiny = torch.finfo(dtype).tiny
+    g64 = got.to(torch.float64)
+    flushed = ((g64 - low.to(torch.float64)).abs() <= tiny) | ((g64 - high.to(torch.float64)).abs() <= tiny)
+    ok = torch.isfinite(got) & ((outside <= 1) | flushed)
+    primary = _activate_f64(_epilogue_f64(acc.to(dtype), bias, dtype), activation, approximate).to(dtype)
+    return {
+        "n": got.numel(),
+        "bad": int((~ok).sum()),
+        "exact_frac": float((got == primary).double().mean()) if got.numel() else 1.0,
+        "max_ulp": int(outside.max()) if got.numel() else 0,
+    }
+
+
 def _brute_lib() -> ctypes.CDLL:
     if not BRUTE_LIB.exists():
         subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)

@@ -5,6 +5,13 @@ with ``oracle.fused_linear.reference_cpu`` (torch addmm/mm + GELU on the
 CPU, src/forgeml/ops.py:28-53) on the same seeded inputs, under the gate of
 ``oracle.fused_linear.tolerance``: fp32 rtol 1e-4 / atol 1e-5*sqrt(K), bf16
 rtol 2e-2 / atol 5e-2, fp16 1e-2 / 1e-2; non-finite output always fails.
+
+16-bit outputs are also held to the kernel's epilogue contract at ulp level
+(``oracle.fused_linear.contract_ulp_check``): every element within one ulp of
+act(rnd(rnd(sum) + bias)) for one of the two roundings of the fp64 sum the
+fp32 accumulation can reach, and at least 99 % of elements exactly equal to
+the rounding of the fp64 sum.  That gate sees a wrong GELU form, a skipped
+rounding step or a truncating conversion, which the tolerance gate does not.
 """
 
 from __future__ import annotations
@@ -14,7 +21,7 @@ import torch
 
 from forgeml_amd import kernels
 from forgeml_amd.ir import GraphError
-from oracle.fused_linear import kernel_contract, reference_cpu, tolerance
+from oracle.fused_linear import contract_ulp_check, kernel_contract, reference_cpu, tolerance
 from tests.cases import case_seed, gemm_inputs, to_gpu
 
 pytestmark = pytest.mark.gpu
@@ -29,6 +36,21 @@ def _gate(got: torch.Tensor, expected: torch.Tensor, k: int, what: str):
     assert torch.isfinite(got).all(), f"{what}: non-finite output"
     rtol, atol = tolerance(expected.dtype, k)
     torch.testing.assert_close(got.float(), expected.float(), rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
+
+
+def _built_for(a_d, b_d, config) -> bool:
+    """Whether ``config`` runs these operands; when not, the boundary must refuse it."""
+    try:
+        kernels.plan(a_d, b_d, config)
+    except GraphError as e:
+        assert "not built for this operand layout" in str(e), str(e)
+        return False
+    return True
+
+
+def _contract(got, a, b, bias, activation, approximate, what, acc=None):
+    report = contract_ulp_check(got, a, b, bias, activation, approximate, acc=acc)
+    assert report["bad"] == 0 and report["exact_frac"] >= 0.99, f"{what}: contract {report}"
 
 
 # -- the reference's own GPU kernel tests (tests/test_kernels.py:101-161) ------
@@ -126,6 +148,7 @@ def test_ragged_sweep(gpu, m, n, k, dtype):
     a_d = a.to(gpu)
     layouts = {"nt": to_gpu(b_nt, gpu), "nn": b_nt.contiguous().to(gpu)}
     bias_d = bias.to(gpu)
+    acc = a.double() @ b_nt.double() if dtype != torch.float32 else None
     for with_bias in (False, True):
         for activation in ("none", "gelu"):
             expected = reference_cpu(a, b_nt, bias if with_bias else None, activation)
@@ -134,6 +157,8 @@ def test_ragged_sweep(gpu, m, n, k, dtype):
                 _say(what)
                 got = kernels.matmul(a_d, b_d, bias_d if with_bias else None, activation=activation)
                 _gate(got, expected, k, what)
+                if acc is not None:
+                    _contract(got, a, b_nt, bias if with_bias else None, activation, "none", what, acc=acc)
 
 
 # -- every tile configuration x operand layout ---------------------------------
@@ -171,6 +196,7 @@ def test_every_config_and_layout(gpu, dtype):
     g = torch.Generator().manual_seed(seed + 1)
     bias = (torch.rand(n, generator=g) * 0.2 - 0.1).to(dtype)
     expected = reference_cpu(a, w.t(), bias, "gelu")
+    acc = a.double() @ w.t().double()
     for config in kernels.candidates(dtype):
         for name, make_a, make_b in layouts:
             what = f"{dtype} config={config} layout={name} seed={seed}"
@@ -181,8 +207,14 @@ def test_every_config_and_layout(gpu, dtype):
                 with pytest.raises(GraphError, match="few-row"):
                     kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
                 continue
+            if not _built_for(a_d, b_d, config):
+                with pytest.raises(GraphError, match="not built"):
+                    kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
+                continue
             got = kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=config)
             _gate(got, expected, k, what)
+            if dtype != torch.float32:
+                _contract(got, a, w.t(), bias, "gelu", "none", what, acc=acc)
 
 
 # -- rows not 16-byte aligned, and split K ----------------------------------------
@@ -205,6 +237,10 @@ def test_unaligned_k_layouts(gpu, dtype, m, n, k):
         for name, b_d in layouts.items():
             what = f"M={m} N={n} K={k} {dtype} B={name} config={config} seed={seed}"
             _say(what)
+            if not _built_for(a_d, b_d, config):
+                with pytest.raises(GraphError, match="not built"):
+                    kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=config)
+                continue
             got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=config)
             _gate(got, expected, k, what)
 
@@ -383,6 +419,31 @@ def test_bf16_decoder_mlp(gpu):
     rows = _row_sample(m, 32, seed)
     h_rows = h[rows.to(gpu)].cpu()
     _gate(h_rows, reference_cpu(x[rows], w1.t(), None, "gelu"), d, "up GEMM sampled rows")
+    _contract(h_rows, x[rows], w1.t(), None, "gelu", "none", "up GEMM sampled rows")
     # The down GEMM is checked on the kernel's own H rows (same inputs).
-    _gate(y[rows.to(gpu)], reference_cpu(h_rows, w2.t(), b2), f, "down GEMM sampled rows")
+    y_rows = y[rows.to(gpu)].cpu()
+    _gate(y_rows, reference_cpu(h_rows, w2.t(), b2), f, "down GEMM sampled rows")
+    _contract(y_rows, h_rows, w2.t(), b2, "none", "none", "down GEMM sampled rows")
     assert torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_gelu_tail_contract(gpu, dtype, approximate):
+    """Pre-activations spanning [-10, 4] (the GELU tail, where x Phi(x) is
+    small) through the tiled, few-row and split-K epilogues: C = A[:, 0]
+    exactly, B selecting column 0 of A."""
+    for m, n, k, layout in ((4096, 64, 8, "nt"), (64, 48, 8, "nt"), (5, 640, 3000, "nn")):
+        vals = torch.linspace(-10.0, 4.0, m)
+        a = torch.zeros(m, k)
+        a[:, 0] = vals
+        w = torch.zeros(n, k)
+        w[:, 0] = 1.0
+        a, w = a.to(dtype), w.to(dtype)
+        b = w.t() if layout == "nt" else w.t().contiguous()
+        a_d, b_d = a.to(gpu), to_gpu(b, gpu)
+        kind = kernels.plan(a_d, b_d)
+        what = f"GELU tail {dtype} {approximate} M={m} N={n} K={k} {kind['kernel']} splits={kind['k_splits']}"
+        _say(what)
+        got = kernels.matmul(a_d, b_d, activation="gelu", approximate=approximate).cpu()
+        _contract(got, a, b, None, "gelu", approximate, what)

@@ -113,6 +113,11 @@ def test_split_k_needs_workspace():
     need = lib.forgeml_hip_gemm_workspace_size(m, n, k, _native.DTYPE_F32, -1)
     assert need > 0
     # B stored [K, N] (N-contiguous): the tiled kernels run it, splitting K.
+    # The plan must confirm the split before any dummy-pointer call: without
+    # it the workspace check would not stop the launch.
+    out = (ctypes.c_int64 * 4)()
+    assert lib.forgeml_hip_gemm_plan(dummy, k, 1, dummy, n, 1, m, n, k, _native.DTYPE_F32, -1, out) == _native.OK
+    assert out[1] > 1 and out[2] > 0, "this layout no longer splits K: the calls below would launch"
     rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, n, 1, None, 0, dummy, m, n, k, 0, 1, -1, None, 0, None)
     assert rc == _native.EWORKSPACE and "workspace" in _native.last_error()
     rc = lib.forgeml_hip_gemm(dummy, k, 1, dummy, n, 1, None, 0, dummy, m, n, k, 0, 1, -1, dummy, need - 4, None)
@@ -220,9 +225,49 @@ def test_launch_size_limits():
     assert lib.forgeml_hip_select_config(16, 1 << 27, 16, bf16) == cid
     rc, (_, _, _, kind) = plan(16, 1 << 25, 16, 16, bf16, few_row)
     assert rc == _native.OK and kind == 1
+    # 16-bit odd K: element loads, built for the 64x64 tile only.  2^18 x 2^18
+    # outputs need 2^32 work-items there, so AUTO refuses with a clear error;
+    # half the rows fit.
+    rc, _ = plan(1 << 18, 1 << 18, 15, 15, bf16, -1)
+    assert rc == _native.EINVAL and "every tile" in _native.last_error()
+    rc, (cid, _, _, _) = plan(1 << 17, 1 << 18, 15, 15, bf16, -1)
+    assert rc == _native.OK and kernels.CANDIDATES[cid].block_m == 64
+    # select_config skips tiles past the bound (fp32 64x64 would need 2^32).
+    cid = lib.forgeml_hip_select_config(1 << 18, 1 << 18, 64, f32)
+    assert cid >= 0 and kernels.CANDIDATES[cid].block_m >= 128
     # Attention: one 256-thread workgroup per query block.
     dummy = ctypes.c_void_p(256)
     st = (ctypes.c_int64 * 4)(1 << 20, 512 * 32, 32, 1)
     args = (dummy, st, dummy, st, dummy, st, dummy, st)
     assert lib.forgeml_hip_attention(*args, 1 << 20, 16, 512, 512, 32, 0, 0.125, f32, None) == _native.EINVAL
     assert "query blocks" in _native.last_error()
+
+
+def test_tiles_refuse_layouts_they_are_not_built_for():
+    """16-bit tiles above 64x64 are not built for element loads (an odd K), and
+    the 8-wave 16-bit tile only for two K-contiguous operands with 16-byte
+    rows: an explicit request is refused with ECONFIG; AUTO plans a built
+    tile (host-side planning only: nothing is launched)."""
+    lib = _native.load()
+    out = (ctypes.c_int64 * 4)()
+    dummy = ctypes.c_void_p(256)
+    bf16 = _native.DTYPE_BF16
+    ids = {(cfg.block_m, cfg.num_waves): kernels.config_id(cfg, torch.bfloat16)
+           for cfg in kernels.candidates(torch.bfloat16) if cfg.block_n == cfg.block_m}
+
+    def plan(k, sbk, sbn, cid):
+        # A row-major [M, K]; B with strides (sbk, sbn); M = N = 1024.
+        return lib.forgeml_hip_gemm_plan(dummy, k, 1, dummy, sbk, sbn, 1024, 1024, k, bf16, cid, out)
+
+    for (bm, waves), cid in ids.items():
+        # Odd K: 16-bit rows only 2-byte aligned, element loads for A.
+        refused = bm > 64
+        assert (plan(1531, 1, 1531, cid) == _native.ECONFIG) == refused, (bm, waves)
+        if refused:
+            assert "not built for this operand layout" in _native.last_error()
+        # B stored [K, N]: the transposing loader.
+        assert (plan(1024, 1024, 1, cid) == _native.ECONFIG) == (waves > 4), (bm, waves)
+        # Both K-contiguous with 16-byte rows: every tile.
+        assert plan(1024, 1, 1024, cid) == _native.OK
+    # AUTO picks a built tile for the odd-K layout.
+    assert plan(1531, 1, 1531, -1) == _native.OK and kernels.CANDIDATES[out[0]].block_m == 64

@@ -16,6 +16,7 @@ Checks, each chosen so a plausible restatement mistake fails one of them:
 
 from __future__ import annotations
 
+import math
 from pathlib import Path
 
 import numpy as np
@@ -149,3 +150,118 @@ def test_tolerances():
     assert tolerance(torch.bfloat16, 14336) == (2e-2, 5e-2)
     with pytest.raises(ValueError):
         tolerance(torch.int32, 4)
+
+
+# -- the ulp-level contract check for 16-bit outputs ---------------------------
+#
+# A faithful CPU model of the kernels' 16-bit epilogue (fp32 sums in another
+# order, one rounding, fp32 bias add and rounding, the relative-accurate fp32
+# GELU forms) must pass contract_ulp_check; the same model with one mistake
+# planted must fail it.  The models live here, on the CPU, only to pin the
+# checker.
+
+_NR_ERFC = (0.17087277, -0.82215223, 1.48851587, -1.13520398, 0.27886807, -0.18628806, 0.09678418,
+            0.37409196, 1.00002368, -1.26551223)
+
+
+def _phi_neg_chebyshev(x: np.ndarray) -> np.ndarray:
+    """Phi(-|x|) in fp32 from the Chebyshev erfc fit of Numerical Recipes 6.2."""
+    z = np.abs(x).astype(np.float32) * np.float32(0.7071067811865476)
+    t = np.float32(1) / (np.float32(1) + np.float32(0.5) * z)
+    p = np.float32(_NR_ERFC[0])
+    for c in _NR_ERFC[1:]:
+        p = (p * t + np.float32(c)).astype(np.float32)
+    return (np.float32(0.5) * t * np.exp(-z * z + p)).astype(np.float32)
+
+
+def _phi_neg_as7126(x: np.ndarray) -> np.ndarray:
+    """Phi(-|x|) from Abramowitz & Stegun 7.1.26 (absolute error 1.5e-7)."""
+    z = np.abs(x).astype(np.float32) * np.float32(0.7071067811865476)
+    t = np.float32(1) / (np.float32(1) + np.float32(0.3275911) * z)
+    poly = ((((1.061405429 * t - 1.453152027) * t + 1.421413741) * t - 0.284496736) * t + 0.254829592)
+    return (0.5 * poly * t * np.exp(-z * z)).astype(np.float32)
+
+
+def _model_16bit(a, b, bias, approximate, *, form=None, skip_round=False, truncate=False):
+    dtype = a.dtype
+    acc = a.float() @ b.float()
+    if truncate:
+        v = (acc.view(torch.int32) & ~0xFFFF).view(torch.float32) if dtype == torch.bfloat16 else acc.to(dtype).float()
+    elif skip_round:
+        v = acc
+    else:
+        v = acc.to(dtype).float()
+    if bias is not None:
+        v = (v + bias.float()).to(dtype).float()
+    x = v.numpy().astype(np.float32)
+    form = form or ("tanh" if approximate == "tanh" else "chebyshev")
+    if form == "tanh":
+        u = np.float32(0.7978845608028654) * (x + np.float32(0.044715) * x * x * x)
+        y = x / (np.float32(1) + np.exp(np.float32(-2) * u))
+    else:
+        q = _phi_neg_chebyshev(x) if form == "chebyshev" else _phi_neg_as7126(x)
+        y = x * np.where(x >= 0, np.float32(1) - q, q)
+    return torch.from_numpy(y.astype(np.float32)).to(dtype)
+
+
+def _contract_inputs(dtype, tail: bool):
+    if tail:
+        # Pre-activations spanning the GELU tail: C = A[:, 0] exactly (K = 2, B selects column 0).
+        vals = torch.linspace(-10.0, 4.0, 3001)
+        a = torch.stack([vals, torch.zeros_like(vals)], 1).to(dtype)
+        b = torch.zeros(2, 8)
+        b[0] = 1.0
+        return a, b.to(dtype), None
+    g = torch.Generator().manual_seed(11)
+    k = 1024
+    a = (torch.randn(200, k, generator=g) * k ** -0.25).to(dtype)
+    b = (torch.randn(k, 96, generator=g) * k ** -0.25).to(dtype)
+    bias = (torch.rand(96, generator=g) * 0.2 - 0.1).to(dtype)
+    return a, b, bias
+
+
+def _passes(report) -> bool:
+    return report["bad"] == 0 and report["exact_frac"] >= 0.99
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+@pytest.mark.parametrize("tail", [False, True])
+def test_contract_check_accepts_the_faithful_model(dtype, approximate, tail):
+    from oracle.fused_linear import contract_ulp_check
+
+    a, b, bias = _contract_inputs(dtype, tail)
+    report = contract_ulp_check(_model_16bit(a, b, bias, approximate), a, b, bias, "gelu", approximate)
+    assert _passes(report), report
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mistake", ["tanh_for_erf", "as7126_gelu", "skip_first_round", "truncate"])
+def test_contract_check_rejects_planted_mistakes(dtype, mistake):
+    from oracle.fused_linear import contract_ulp_check
+
+    if mistake == "truncate" and dtype == torch.float16:
+        pytest.skip("the truncating conversion is modelled for bf16 only")
+    tail = mistake == "as7126_gelu"  # the absolute-error fit only shows in the tail
+    a, b, bias = _contract_inputs(dtype, tail)
+    kw = {"tanh_for_erf": {"form": "tanh"}, "as7126_gelu": {"form": "as7126"},
+          "skip_first_round": {"skip_round": True}, "truncate": {"truncate": True}}[mistake]
+    report = contract_ulp_check(_model_16bit(a, b, bias, "none", **kw), a, b, bias, "gelu", "none")
+    assert not _passes(report), report
+
+
+def test_gelu_f64_is_exact_in_the_tail():
+    from oracle.fused_linear import gelu_f64
+
+    # x Phi(x) at table values of the normal CDF, including far tails.
+    phi = {-8.0: 6.22096057427178e-16, -5.0: 2.866515718791939e-07, -3.0: 0.0013498980316300946,
+           1.0: 0.8413447460685429}
+    for x, p in phi.items():
+        got = gelu_f64(torch.tensor([x], dtype=torch.float64)).item()
+        assert got == pytest.approx(x * p, rel=1e-13)
+    xs = torch.linspace(-12, 12, 97, dtype=torch.float64)
+    tanh_form = gelu_f64(xs, "tanh")
+    u = math.sqrt(2 / math.pi) * (xs + 0.044715 * xs ** 3)
+    direct = 0.5 * xs * (1 + torch.tanh(u))
+    mask = xs > -3  # where the direct form does not cancel
+    torch.testing.assert_close(tanh_form[mask], direct[mask], rtol=1e-13, atol=1e-15)
