@@ -1,25 +1,34 @@
-"""Per-node tile selection with a correctness gate before any timing.
+"""Per-node tile selection: a correctness gate first, then timing.
 
-Follows ForgeML's ``tune_graph`` (src/forgeml/autotune.py:16-103): each GEMM
-node planned for the GPU kernel is evaluated once with the torch path for its
-expected value; every candidate tile is launched into a fresh output and must
-pass ``check_output`` before it may be timed; a launch that raises is
-recorded as a rejection; the lowest median wins (first candidate on ties);
-downstream nodes receive the torch value as input.  The winners are stored
-in ``compiled.kernel_configs`` for this compiled model only (no cache).
+The contract is ForgeML's ``tune_graph`` (src/forgeml/autotune.py:16-103):
 
-The candidate set is the MI355X tile table built for the node's dtype
-(``kernels.candidates``), not Triton meta-parameters.
+* the compiled model runs once, then the graph is walked with torch values,
+  so every GEMM node is tuned on the inputs it sees in a real call and
+  downstream nodes receive the torch result;
+* each candidate launches into a fresh output and must pass the gate
+  (``measurement.check_output`` against the torch value) before it may be
+  timed; an exception from the launch or the gate rejects it;
+* the winner is the lowest median latency, the earliest candidate on ties,
+  and is stored in ``compiled.kernel_configs`` of this instance only;
+* the report keeps the reference's schema (``scope``, ``timing``,
+  ``warmup``, ``repeats``, ``nodes[*]`` with ``winner``, ``config``,
+  ``candidates``, ``rejected``, input shapes and strides, dtype, device,
+  activation, approximate).
+
+The search space is the tile table built for the node's dtype
+(``kernels.candidates``).
 """
 
 from __future__ import annotations
 
-from dataclasses import asdict
+from collections.abc import Callable
+from dataclasses import asdict, dataclass
 from typing import TYPE_CHECKING
 
 import torch
 
 from forgeml_amd import kernels
+from forgeml_amd.kernels import KernelConfig
 from forgeml_amd.measurement import check_output, measure_variants
 from forgeml_amd.ops import evaluate
 
@@ -27,70 +36,98 @@ if TYPE_CHECKING:
     from forgeml_amd.compiler import CompiledModel
 
 
+@dataclass(frozen=True)
+class _GemmNode:
+    """A GEMM node's operands as a tuning call sees them."""
+
+    a: torch.Tensor
+    b: torch.Tensor
+    bias: torch.Tensor | None
+    activation: str
+    approximate: str
+
+    @classmethod
+    def of(cls, node, args: tuple[torch.Tensor, ...]) -> "_GemmNode":
+        gelu = node.op == "fused_linear_gelu"
+        return cls(args[0], args[1], args[2] if len(args) == 3 else None,
+                   "gelu" if gelu else "none", node.attrs.get("approximate", "none") if gelu else "none")
+
+    def launcher(self, config: KernelConfig) -> Callable[[], torch.Tensor]:
+        # kernels.matmul is looked up at call time, so a replacement installed
+        # on the module (tests do this) is what runs.
+        return lambda: kernels.matmul(self.a, self.b, self.bias, activation=self.activation,
+                                      approximate=self.approximate, config=config)
+
+    def describe(self, args) -> dict:
+        return {
+            "input_shapes": [list(t.shape) for t in args],
+            "input_strides": [list(t.stride()) for t in args],
+            "dtype": str(self.a.dtype),
+            "device": str(self.a.device),
+            "activation": self.activation,
+            "approximate": self.approximate,
+        }
+
+
+def _gate(call: _GemmNode, expected: torch.Tensor):
+    """Launch every candidate once against ``expected``: (passing, rejected)."""
+    passing: dict[str, tuple[KernelConfig, Callable, dict]] = {}
+    rejected: dict[str, str] = {}
+    for idx, config in enumerate(kernels.candidates(call.a.dtype)):
+        label = f"candidate_{idx}"
+        launch = call.launcher(config)
+        try:
+            verdict = check_output(launch(), expected)
+        except Exception as exc:  # noqa: BLE001 - a launch or gate failure rejects this candidate only
+            rejected[label] = str(exc)
+        else:
+            passing[label] = (config, launch, verdict)
+    return passing, rejected
+
+
+def _winner(timings: dict[str, dict], order: list[str]) -> str:
+    return min(order, key=lambda label: (timings[label]["median_ms"], order.index(label)))
+
+
 @torch.inference_mode()
-def tune_graph(
-    compiled: CompiledModel,
-    inputs: tuple[torch.Tensor, ...],
-    *,
-    warmup: int = 3,
-    repeats: int = 10,
-) -> dict:
+def tune_graph(compiled: CompiledModel, inputs: tuple[torch.Tensor, ...], *, warmup: int = 3,
+               repeats: int = 10) -> dict:
+    """Gate, time and pick a tile for every hip GEMM node of ``compiled``."""
     if warmup < 0 or repeats < 2:
         raise ValueError("autotuning requires warmup >= 0 and repeats >= 2")
-    compiled(*inputs)
-    values = dict(compiled.graph.constants)
-    values.update(zip(compiled.graph.inputs, inputs))
-    records: dict = {}
-    chosen: dict = {}
+    compiled(*inputs)  # the model must run as compiled before any node is tuned
+    env = {**compiled.graph.constants, **dict(zip(compiled.graph.inputs, inputs))}
+    nodes_report: dict[str, dict] = {}
+    picked: dict[str, KernelConfig] = {}
     for node in compiled.graph.nodes:
-        args = tuple(values[name] for name in node.inputs)
-        expected = evaluate(node.op, args, node.attrs)
-        if compiled.kernel_plan.get(node.name) == "hip" and node.op in kernels.GEMM_OPS:
-            bias = args[2] if len(args) == 3 else None
-            activation = "gelu" if node.op == "fused_linear_gelu" else "none"
-            approximate = node.attrs.get("approximate", "none") if activation == "gelu" else "none"
-            variants, configs, rejected, errors = {}, {}, {}, {}
-            for index, config in enumerate(kernels.candidates(args[0].dtype)):
-                name = f"candidate_{index}"
-
-                def launch(config=config, args=args, bias=bias, activation=activation, approximate=approximate):
-                    return kernels.matmul(
-                        args[0], args[1], bias, activation=activation, approximate=approximate, config=config
-                    )
-
-                try:
-                    errors[name] = check_output(launch(), expected)
-                except Exception as exc:  # noqa: BLE001 - any failure rejects the candidate
-                    rejected[name] = str(exc)
-                    continue
-                variants[name] = launch
-                configs[name] = config
-            if not variants:
-                raise RuntimeError(f"no numerically valid kernel candidate for {node.name!r}")
-            timings = measure_variants(variants, device=args[0].device, warmup=warmup, repeats=repeats)
-            winner = min(timings, key=lambda name: timings[name]["median_ms"])
-            chosen[node.name] = configs[winner]
-            records[node.name] = {
-                "winner": winner,
-                "config": asdict(configs[winner]),
-                "candidates": {
-                    name: {"config": asdict(configs[name]), "timing": timing, "correctness": errors[name]}
-                    for name, timing in timings.items()
-                },
-                "rejected": rejected,
-                "input_shapes": [list(arg.shape) for arg in args],
-                "input_strides": [list(arg.stride()) for arg in args],
-                "dtype": str(args[0].dtype),
-                "device": str(args[0].device),
-                "activation": activation,
-                "approximate": approximate,
-            }
-        values[node.name] = expected
-    compiled.kernel_configs.update(chosen)
+        args = tuple(env[name] for name in node.inputs)
+        reference = evaluate(node.op, args, node.attrs)
+        env[node.name] = reference
+        if node.op not in kernels.GEMM_OPS or compiled.kernel_plan.get(node.name) != "hip":
+            continue
+        call = _GemmNode.of(node, args)
+        passing, rejected = _gate(call, reference)
+        if not passing:
+            raise RuntimeError(f"no numerically valid kernel candidate for {node.name!r}")
+        timings = measure_variants({label: launch for label, (_, launch, _) in passing.items()},
+                                   device=call.a.device, warmup=warmup, repeats=repeats)
+        best = _winner(timings, list(passing))
+        picked[node.name] = passing[best][0]
+        nodes_report[node.name] = {
+            "winner": best,
+            "config": asdict(passing[best][0]),
+            "candidates": {
+                label: {"config": asdict(config), "timing": timings[label], "correctness": verdict}
+                for label, (config, _, verdict) in passing.items()
+            },
+            "rejected": rejected,
+            **call.describe(args),
+        }
+    compiled.kernel_configs.update(picked)
     return {
         "scope": "this_compiled_model_instance_only",
         "timing": "synchronized_host_wall_clock_including_output_allocation",
         "warmup": warmup,
         "repeats": repeats,
-        "nodes": records,
+        "nodes": nodes_report,
     }

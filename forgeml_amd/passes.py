@@ -1,25 +1,40 @@
 """Graph passes that produce the GEMM nodes the gfx950 kernels execute.
 
-The pipeline and every rewrite keep the semantics of ForgeML's
-``optimize`` (src/forgeml/passes.py:410-430) so that a model compiles to the
-same graph, with the same node names, as under the reference:
+A model must compile to the same graph, node names and memory plan as under
+ForgeML's ``optimize`` (src/forgeml/passes.py:410-430), whose published
+captures pin them.  So the pipeline, the rewrite rules and the generated
+names are ForgeML's:
 
-1. dead-node elimination (passes.py:33-42)
-2. constant folding under a 64 MiB cap (passes.py:45-74)
-3. algebraic simplification of reshapes/transposes (passes.py:83-124)
-4. common-subexpression elimination (passes.py:135-161)
-5. ``canonicalize_linear``: matmul + 1-D bias add -> linear (passes.py:164-201)
-6. ``fuse_linear_gelu``: linear/matmul (+ bias add) + gelu -> one
-   ``fused_linear_gelu`` node (passes.py:204-265)
-7. ``fuse_shared_projections``: linears that share an input and constant
-   weights -> one wide linear plus ``narrow`` views (passes.py:268-339), the
-   fused QKV projection
-8. ``schedule``: the topological order with the smallest planned arena among
-   six greedy orders (passes.py:342-407)
+1. dead-node elimination;
+2. constant folding of nodes whose inputs are all constants, views always,
+   other ops while input and output stay within 64 MiB;
+3. algebraic simplification: identity reshapes and transposes vanish, a
+   reshape of a reshape reads the first one's source, an inverse transpose
+   pair vanishes;
+4. common-subexpression elimination (``add`` / ``mul`` operands unordered);
+5. ``canonicalize_linear``: ``matmul`` + 1-D output-width bias ``add`` ->
+   ``linear`` (passes.py:164-201);
+6. ``fuse_linear_gelu``: ``gelu`` of a ``linear`` / ``matmul`` (or of a
+   ``matmul`` + constant bias ``add``) whose result nothing else reads ->
+   ``fused_linear_gelu`` under the gelu's name (passes.py:204-265);
+7. ``fuse_shared_projections``: ``linear`` nodes with constant weights that
+   read the same input -> one wide ``<leader>_shared_<n>`` linear plus
+   ``narrow`` views under the members' names (passes.py:268-339): the fused
+   QKV projection;
+8. ``schedule``: among six greedy topological orders, the one with the
+   smallest planned arena, then the lexicographically smallest names
+   (passes.py:342-407).
+
+How it is built here: every pass works on a ``_Work`` copy of the graph (an
+ordered node list, an alias map that later nodes are read through, and
+consumer counts), rewrites in one sweep, and commits a validated ``Graph``
+whose constants are pruned to what is still read.
 """
 
 from __future__ import annotations
 
+from collections import Counter
+from collections.abc import Callable
 from dataclasses import dataclass
 
 import torch
@@ -38,363 +53,401 @@ class PassRecord:
     nodes_after: int
 
 
-def _with_nodes(graph: Graph, nodes: list[Node], constants: dict, outputs=None) -> Graph:
-    out = Graph(
-        inputs=dict(graph.inputs),
-        constants=constants,
-        nodes=nodes,
-        outputs=tuple(graph.outputs if outputs is None else outputs),
-        output_is_tuple=graph.output_is_tuple,
-    )
-    out.validate()
-    return out
+class _Work:
+    """A graph being rewritten."""
+
+    def __init__(self, graph: Graph):
+        self.source = graph
+        self.constants = dict(graph.constants)
+        self.nodes: list[Node] = []
+        self._alias: dict[str, str] = {}
+
+    # Names read by later nodes go through the alias map.
+    def alias(self, name: str, target: str) -> None:
+        self._alias[name] = target
+
+    def resolve(self, name: str) -> str:
+        seen = name
+        while seen in self._alias and self._alias[seen] != seen:
+            seen = self._alias[seen]
+        return seen
+
+    def keep(self, node: Node) -> Node:
+        node = Node(node.name, node.op, tuple(self.resolve(i) for i in node.inputs), dict(node.attrs), node.spec)
+        self.nodes.append(node)
+        return node
+
+    def commit(self, *, prune_constants: bool = True, outputs: tuple[str, ...] | None = None) -> Graph:
+        outs = tuple(self.resolve(o) for o in (self.source.outputs if outputs is None else outputs))
+        constants = self.constants
+        if prune_constants:
+            read = {i for n in self.nodes for i in n.inputs} | set(outs)
+            constants = {k: v for k, v in constants.items() if k in read}
+        graph = Graph(inputs=dict(self.source.inputs), constants=constants, nodes=list(self.nodes), outputs=outs,
+                      output_is_tuple=self.source.output_is_tuple)
+        graph.validate()
+        return graph
 
 
-def _consumers(graph: Graph) -> dict[str, list[str]]:
-    table: dict[str, list[str]] = {}
-    for node in graph.nodes:
-        for src in node.inputs:
-            table.setdefault(src, []).append(node.name)
-    return table
+def _readers(graph: Graph) -> Counter:
+    """How many node inputs read each name (a node reading a name twice counts twice)."""
+    return Counter(i for n in graph.nodes for i in n.inputs)
 
 
-def _follow(aliases: dict[str, str], name: str) -> str:
-    while aliases.get(name, name) != name:
-        name = aliases[name]
-    return name
+def _sole_reader(graph: Graph, readers: Counter, name: str) -> bool:
+    """The value feeds exactly one input slot and is not a graph output."""
+    return readers[name] == 1 and name not in graph.outputs
 
+
+# -- clean-up passes --------------------------------------------------------------
 
 def eliminate_dead_nodes(graph: Graph) -> Graph:
-    live = set(graph.outputs)
-    kept: list[Node] = []
-    for node in reversed(graph.nodes):
-        if node.name in live:
-            kept.append(node)
-            live.update(node.inputs)
-    kept.reverse()
-    return _with_nodes(graph, kept, {k: v for k, v in graph.constants.items() if k in live})
+    """Drop nodes and constants the outputs do not depend on."""
+    producer = {n.name: n for n in graph.nodes}
+    live: set[str] = set()
+    stack = list(graph.outputs)
+    while stack:
+        name = stack.pop()
+        if name in live:
+            continue
+        live.add(name)
+        if name in producer:
+            stack.extend(producer[name].inputs)
+    work = _Work(graph)
+    work.nodes = [n for n in graph.nodes if n.name in live]
+    work.constants = {k: v for k, v in graph.constants.items() if k in live}
+    return work.commit(prune_constants=False)
+
+
+def _foldable(node: Node, known: dict[str, torch.Tensor]) -> bool:
+    if not all(i in known for i in node.inputs):
+        return False
+    if node.op in VIEW_LIKE_OPS:
+        return True  # a view materialises nothing
+    read = sum(known[i].numel() * known[i].element_size() for i in set(node.inputs))
+    return node.spec.nbytes <= FOLD_LIMIT_BYTES and read <= FOLD_LIMIT_BYTES
 
 
 def fold_constants(graph: Graph) -> Graph:
-    constants = dict(graph.constants)
-    known = dict(constants)
-    nodes: list[Node] = []
+    """Evaluate, once, every node computable from constants (within the size cap)."""
+    work = _Work(graph)
     for node in graph.nodes:
-        if not all(src in known for src in node.inputs):
-            nodes.append(node)
-            continue
-        # Views materialise nothing; other ops are folded only under the cap,
-        # which bounds both compile-time memory and fold compute.
-        in_bytes = sum(known[s].numel() * known[s].element_size() for s in dict.fromkeys(node.inputs))
-        if node.op not in VIEW_LIKE_OPS and (
-            node.spec.nbytes > FOLD_LIMIT_BYTES or in_bytes > FOLD_LIMIT_BYTES
-        ):
-            nodes.append(node)
+        if not _foldable(node, work.constants):
+            work.nodes.append(node)
             continue
         try:
             with torch.inference_mode():
-                value = evaluate(node.op, tuple(known[s] for s in node.inputs), dict(node.attrs))
-        except Exception as e:  # noqa: BLE001
+                work.constants[node.name] = evaluate(node.op, tuple(work.constants[i] for i in node.inputs),
+                                                     dict(node.attrs))
+        except Exception as e:  # noqa: BLE001 - report which node could not be folded
             raise GraphError(f"constant folding failed at node {node.name!r}: {e}") from e
-        constants[node.name] = value
-        known[node.name] = value
-    used = {s for n in nodes for s in n.inputs} | set(graph.outputs)
-    return _with_nodes(graph, nodes, {k: v for k, v in constants.items() if k in used})
+    return work.commit()
+
+
+# Peephole rules of simplify_algebra: given the node (inputs already
+# resolved) and the kept producers, return the name it is an alias of, a
+# replacement node, or the node itself.
+def _simplify_reshape(node: Node, producer: Node | None, specs) -> str | Node:
+    if specs[node.inputs[0]].shape == node.spec.shape:
+        return node.inputs[0]
+    if producer is not None and producer.op == "reshape":
+        return Node(node.name, "reshape", producer.inputs, dict(node.attrs), node.spec)
+    return node
+
+
+def _transpose_axes(node: Node, rank: int) -> frozenset:
+    return frozenset((node.attrs["dim0"] % rank, node.attrs["dim1"] % rank))
+
+
+def _simplify_transpose(node: Node, producer: Node | None, specs) -> str | Node:
+    rank = len(node.spec.shape)
+    axes = _transpose_axes(node, rank)
+    if len(axes) == 1:
+        return node.inputs[0]
+    if producer is not None and producer.op == "transpose" and _transpose_axes(producer, rank) == axes:
+        return producer.inputs[0]
+    return node
+
+
+_PEEPHOLES: dict[str, Callable] = {"reshape": _simplify_reshape, "transpose": _simplify_transpose}
 
 
 def simplify_algebra(graph: Graph) -> Graph:
     specs = graph.specs()
-    aliases: dict[str, str] = {}
+    work = _Work(graph)
     kept: dict[str, Node] = {}
-    nodes: list[Node] = []
     for original in graph.nodes:
-        inputs = tuple(_follow(aliases, s) for s in original.inputs)
-        node = Node(original.name, original.op, inputs, dict(original.attrs), original.spec)
-        if node.op == "reshape":
-            if specs[node.inputs[0]].shape == node.spec.shape:
-                aliases[node.name] = node.inputs[0]  # identity reshape
-                continue
-            src = kept.get(node.inputs[0])
-            if src is not None and src.op == "reshape":  # reshape of reshape
-                node = Node(node.name, "reshape", src.inputs, dict(node.attrs), node.spec)
-        elif node.op == "transpose":
-            rank = len(node.spec.shape)
-            dims = frozenset((node.attrs["dim0"] % rank, node.attrs["dim1"] % rank))
-            if len(dims) == 1:
-                aliases[node.name] = node.inputs[0]  # transpose(d, d)
-                continue
-            src = kept.get(node.inputs[0])
-            if (
-                src is not None
-                and src.op == "transpose"
-                and frozenset((src.attrs["dim0"] % rank, src.attrs["dim1"] % rank)) == dims
-            ):
-                aliases[node.name] = _follow(aliases, src.inputs[0])  # inverse pair
-                continue
-        aliases[node.name] = node.name
-        kept[node.name] = node
-        nodes.append(node)
-    outputs = tuple(_follow(aliases, name) for name in graph.outputs)
-    rewritten = Graph(
-        inputs=dict(graph.inputs),
-        constants=dict(graph.constants),
-        nodes=nodes,
-        outputs=outputs,
-        output_is_tuple=graph.output_is_tuple,
-    )
-    rewritten.validate()
-    return eliminate_dead_nodes(rewritten)
+        node = Node(original.name, original.op, tuple(work.resolve(i) for i in original.inputs),
+                    dict(original.attrs), original.spec)
+        rule = _PEEPHOLES.get(node.op)
+        result = node if rule is None else rule(node, kept.get(node.inputs[0]), specs)
+        if isinstance(result, str):
+            work.alias(node.name, work.resolve(result))
+            continue
+        kept[result.name] = work.keep(result)
+    return eliminate_dead_nodes(work.commit(prune_constants=False))
 
 
-def _hashable(value):
-    if isinstance(value, (tuple, list)):
-        return tuple(_hashable(v) for v in value)
+def _frozen(value):
     if isinstance(value, dict):
-        return tuple(sorted((k, _hashable(v)) for k, v in value.items()))
+        return tuple(sorted((k, _frozen(v)) for k, v in value.items()))
+    if isinstance(value, (list, tuple)):
+        return tuple(_frozen(v) for v in value)
     return value
 
 
+_COMMUTATIVE = frozenset({"add", "mul"})
+
+
 def common_subexpression_elimination(graph: Graph) -> Graph:
-    aliases: dict[str, str] = {}
-    first_of: dict[tuple, str] = {}
-    nodes: list[Node] = []
+    work = _Work(graph)
+    first: dict[tuple, str] = {}
     for node in graph.nodes:
-        inputs = tuple(_follow(aliases, s) for s in node.inputs)
-        operands = tuple(sorted(inputs)) if node.op in ("add", "mul") else inputs
-        key = (node.op, operands, _hashable(node.attrs), node.spec)
-        if key in first_of:
-            aliases[node.name] = first_of[key]
-            continue
-        first_of[key] = node.name
-        aliases[node.name] = node.name
-        nodes.append(Node(node.name, node.op, inputs, dict(node.attrs), node.spec))
-    outputs = tuple(_follow(aliases, name) for name in graph.outputs)
-    used = {s for n in nodes for s in n.inputs} | set(outputs)
-    return _with_nodes(graph, nodes, {k: v for k, v in graph.constants.items() if k in used}, outputs)
+        inputs = tuple(work.resolve(i) for i in node.inputs)
+        key = (node.op, tuple(sorted(inputs)) if node.op in _COMMUTATIVE else inputs, _frozen(node.attrs), node.spec)
+        if key in first:
+            work.alias(node.name, first[key])
+        else:
+            first[key] = node.name
+            work.keep(node)
+    return work.commit()
 
 
-def _only_consumer(graph: Graph, consumers: dict[str, list[str]], name: str) -> bool:
-    return name not in graph.outputs and len(consumers.get(name, ())) == 1
+# -- the GEMM rewrites -------------------------------------------------------------------
+
+def _replace_and_drop(graph: Graph, replaced: dict[str, Node], dropped: set[str]) -> Graph:
+    work = _Work(graph)
+    work.nodes = [replaced.get(n.name, n) for n in graph.nodes if n.name not in dropped]
+    return work.commit()
 
 
 def canonicalize_linear(graph: Graph) -> Graph:
-    """matmul(x, w) + b with a 1-D output-width b becomes linear(x, w, b)."""
-    consumers = _consumers(graph)
-    by_name = {n.name: n for n in graph.nodes}
+    """add(matmul(x, w), b) with b 1-D of the output width -> linear(x, w, b)."""
+    producer = {n.name: n for n in graph.nodes}
+    readers = _readers(graph)
     specs = graph.specs()
     replaced: dict[str, Node] = {}
     dropped: set[str] = set()
     for node in graph.nodes:
         if node.op != "add":
             continue
-        x, y = node.inputs
-        for mm_name, bias in ((x, y), (y, x)):
-            mm = by_name.get(mm_name)
-            bias_spec = specs.get(bias)
-            if mm is None or mm.op != "matmul" or not _only_consumer(graph, consumers, mm.name):
+        a, b = node.inputs
+        for gemm_name, bias in ((a, b), (b, a)):
+            gemm = producer.get(gemm_name)
+            if gemm is None or gemm.op != "matmul" or not _sole_reader(graph, readers, gemm_name):
                 continue
-            if bias_spec is None or len(bias_spec.shape) != 1 or bias_spec.shape[0] != mm.spec.shape[1]:
+            bias_shape = specs[bias].shape if bias in specs else None
+            if bias_shape is None or len(bias_shape) != 1 or bias_shape[0] != gemm.spec.shape[1]:
                 continue
-            replaced[node.name] = Node(node.name, "linear", mm.inputs + (bias,), {}, node.spec)
-            dropped.add(mm.name)
+            replaced[node.name] = Node(node.name, "linear", gemm.inputs + (bias,), {}, node.spec)
+            dropped.add(gemm_name)
             break
-    nodes = [replaced.get(n.name, n) for n in graph.nodes if n.name not in dropped]
-    used = {s for n in nodes for s in n.inputs}
-    return _with_nodes(
-        graph, nodes, {k: v for k, v in graph.constants.items() if k in used or k in graph.outputs}
-    )
+    return _replace_and_drop(graph, replaced, dropped)
+
+
+def _matmul_plus_constant_bias(graph: Graph, producer: dict[str, Node], add: Node):
+    """(matmul node, bias name) when ``add`` is matmul + a constant, else None."""
+    a, b = add.inputs
+    for gemm_name, bias in ((a, b), (b, a)):
+        gemm = producer.get(gemm_name)
+        if gemm is not None and gemm.op == "matmul" and bias in graph.constants:
+            return gemm, bias
+    return None
 
 
 def fuse_linear_gelu(graph: Graph) -> Graph:
-    """gelu(linear|matmul) and gelu(matmul + const bias) become fused_linear_gelu.
+    """gelu(linear | matmul) and gelu(matmul + constant bias) -> fused_linear_gelu.
 
     The fused node keeps the gelu node's name, spec and ``approximate``.
     """
-    consumers = _consumers(graph)
-    by_name = {n.name: n for n in graph.nodes}
+    producer = {n.name: n for n in graph.nodes}
+    readers = _readers(graph)
     replaced: dict[str, Node] = {}
     dropped: set[str] = set()
+
+    def fused(gelu: Node, operands: tuple[str, ...]) -> Node:
+        return Node(gelu.name, "fused_linear_gelu", operands, {"approximate": gelu.attrs.get("approximate", "none")},
+                    gelu.spec)
+
     for node in graph.nodes:
-        if node.op != "gelu" or len(node.inputs) != 1:
+        if node.op != "gelu" or len(node.inputs) != 1 or node.inputs[0] not in producer:
             continue
-        approximate = node.attrs.get("approximate", "none")
-        producer = by_name.get(node.inputs[0])
-        if producer is None:
+        src = producer[node.inputs[0]]
+        if not _sole_reader(graph, readers, src.name):
             continue
-        if producer.op in ("linear", "matmul"):
-            if _only_consumer(graph, consumers, producer.name):
-                replaced[node.name] = Node(
-                    node.name, "fused_linear_gelu", producer.inputs, {"approximate": approximate}, node.spec
-                )
-                dropped.add(producer.name)
+        if src.op in ("linear", "matmul"):
+            replaced[node.name] = fused(node, src.inputs)
+            dropped.add(src.name)
             continue
-        if producer.op != "add" or not _only_consumer(graph, consumers, producer.name):
+        if src.op != "add":
             continue
-        match = None
-        for mm_name, bias in ((producer.inputs[0], producer.inputs[1]), (producer.inputs[1], producer.inputs[0])):
-            mm = by_name.get(mm_name)
-            if mm is not None and mm.op == "matmul" and bias in graph.constants:
-                match = (mm, bias)
-                break
+        match = _matmul_plus_constant_bias(graph, producer, src)
         if match is None:
             continue
-        mm, bias = match
-        if not _only_consumer(graph, consumers, mm.name):
+        gemm, bias = match
+        bias_value = graph.constants[bias]
+        if (not _sole_reader(graph, readers, gemm.name) or bias_value.dim() != 1 or len(gemm.spec.shape) != 2
+                or bias_value.shape[0] != gemm.spec.shape[1]):
             continue
-        bias_t = graph.constants[bias]
-        if bias_t.dim() != 1 or bias_t.shape[0] != mm.spec.shape[1] or len(mm.spec.shape) != 2:
+        replaced[node.name] = fused(node, (gemm.inputs[0], gemm.inputs[1], bias))
+        dropped.update((gemm.name, src.name))
+    return _replace_and_drop(graph, replaced, dropped)
+
+
+class _Namer:
+    """``<hint>_<n>`` names from one counter, skipping names already taken."""
+
+    def __init__(self, taken):
+        self.taken = set(taken)
+        self.serial = 0
+
+    def __call__(self, hint: str) -> str:
+        while True:
+            self.serial += 1
+            name = f"{hint}_{self.serial}"
+            if name not in self.taken:
+                self.taken.add(name)
+                return name
+
+
+def _projection_groups(graph: Graph) -> list[list[Node]]:
+    """Linear nodes with constant parameters grouped by (input, arity), in graph order."""
+    groups: dict[tuple[str, int], list[Node]] = {}
+    for node in graph.nodes:
+        if node.op != "linear" or not all(p in graph.constants for p in node.inputs[1:]):
             continue
-        replaced[node.name] = Node(
-            node.name,
-            "fused_linear_gelu",
-            (mm.inputs[0], mm.inputs[1], bias),
-            {"approximate": approximate},
-            node.spec,
-        )
-        dropped.update((mm.name, producer.name))
-    if not replaced:
-        return _with_nodes(graph, list(graph.nodes), dict(graph.constants))
-    nodes = [replaced.get(n.name, n) for n in graph.nodes if n.name not in dropped]
-    used = {s for n in nodes for s in n.inputs}
-    return _with_nodes(
-        graph, nodes, {k: v for k, v in graph.constants.items() if k in used or k in graph.outputs}
-    )
+        groups.setdefault((node.inputs[0], len(node.inputs)), []).append(node)
+    return [members for members in groups.values() if len(members) > 1]
 
 
 def fuse_shared_projections(graph: Graph) -> Graph:
-    """Linears reading the same input with constant weights become one wide GEMM.
+    """Linears reading the same input with constant weights -> one wide GEMM.
 
     Members are concatenated along N in graph order into a ``<leader>_shared``
-    linear; each member becomes a ``narrow`` view of it (so the fused QKV
-    projection is one kernel launch with N = 3 * d_model).
+    linear emitted at the leader's position; each member becomes a
+    ``narrow`` view of it (so the fused QKV projection is one kernel launch
+    with N = 3 * d_model).
     """
-    position = {n.name: i for i, n in enumerate(graph.nodes)}
-    specs = graph.specs()
-    groups: dict[tuple[str, int], list[Node]] = {}
-    for node in graph.nodes:
-        if node.op != "linear" or node.inputs[1] not in graph.constants:
-            continue
-        if len(node.inputs) == 3 and node.inputs[2] not in graph.constants:
-            continue
-        groups.setdefault((node.inputs[0], len(node.inputs)), []).append(node)
-    groups = {k: v for k, v in groups.items() if len(v) >= 2}
+    groups = _projection_groups(graph)
     if not groups:
-        return _with_nodes(graph, list(graph.nodes), dict(graph.constants))
-    taken = set(graph.inputs) | set(graph.constants) | set(position)
+        return _replace_and_drop(graph, {}, set())
+    name = _Namer(set(graph.inputs) | set(graph.constants) | {n.name for n in graph.nodes})
     constants = dict(graph.constants)
-    serial = 0
-
-    def fresh(hint: str) -> str:
-        nonlocal serial
-        while True:
-            serial += 1
-            name = f"{hint}_{serial}"
-            if name not in taken:
-                taken.add(name)
-                return name
-
-    emitted_at: dict[str, list[Node]] = {}
-    dropped: set[str] = set()
-    for members in groups.values():
-        members.sort(key=lambda n: position[n.name])
-        leader = members[0]
-        has_bias = len(leader.inputs) == 3
-        if len({constants[m.inputs[1]].dtype for m in members}) != 1:
-            continue
-        if has_bias and len({constants[m.inputs[2]].dtype for m in members}) > 1:
-            continue
-        x_spec = specs[leader.inputs[0]]
-        weight = fresh(f"{leader.name}_shared_weight")
-        constants[weight] = torch.cat([constants[m.inputs[1]] for m in members], dim=1).contiguous()
-        inputs = [leader.inputs[0], weight]
-        if has_bias:
-            bias = fresh(f"{leader.name}_shared_bias")
-            constants[bias] = torch.cat([constants[m.inputs[2]] for m in members])
-            inputs.append(bias)
-        width = sum(m.spec.shape[1] for m in members)
-        wide = fresh(f"{leader.name}_shared")
-        out = [Node(wide, "linear", tuple(inputs), {}, TensorSpec((x_spec.shape[0], width), x_spec.dtype, x_spec.device))]
-        offset = 0
-        for m in members:
-            out.append(Node(m.name, "narrow", (wide,), {"dim": 1, "start": offset, "length": m.spec.shape[1]}, m.spec))
-            offset += m.spec.shape[1]
-            dropped.add(m.name)
-        emitted_at[leader.name] = out
-    nodes: list[Node] = []
-    for node in graph.nodes:
-        if node.name in emitted_at:
-            nodes.extend(emitted_at[node.name])
-        elif node.name not in dropped:
-            nodes.append(node)
-    return _with_nodes(graph, nodes, constants)
-
-
-def _greedy_order(graph: Graph, score) -> list[Node]:
-    """Topological order picking, among ready nodes, the max of score()."""
-    outputs = set(graph.outputs)
-    position = {n.name: i for i, n in enumerate(graph.nodes)}
-    by_name = {n.name: n for n in graph.nodes}
-    users: dict[str, set[str]] = {}
-    waiting: dict[str, set[str]] = {}
-    for node in graph.nodes:
-        for src in set(node.inputs):
-            users.setdefault(src, set()).add(node.name)
-        waiting[node.name] = {s for s in node.inputs if s in position}
     specs = graph.specs()
-    pending_users = {k: len(v) for k, v in users.items() if k in position}
+    at_leader: dict[str, list[Node]] = {}
+    dropped: set[str] = set()
+    for members in groups:
+        leader = members[0]
+        with_bias = len(leader.inputs) == 3
+        parts = [[constants[m.inputs[j]] for m in members] for j in range(1, len(leader.inputs))]
+        if any(len({t.dtype for t in part}) > 1 for part in parts):
+            continue
+        operands = [leader.inputs[0]]
+        weight = name(f"{leader.name}_shared_weight")
+        constants[weight] = torch.cat(parts[0], dim=1).contiguous()
+        operands.append(weight)
+        if with_bias:
+            bias = name(f"{leader.name}_shared_bias")
+            constants[bias] = torch.cat(parts[1])
+            operands.append(bias)
+        x = specs[leader.inputs[0]]
+        widths = [m.spec.shape[1] for m in members]
+        wide = name(f"{leader.name}_shared")
+        emitted = [Node(wide, "linear", tuple(operands), {}, TensorSpec((x.shape[0], sum(widths)), x.dtype, x.device))]
+        starts = [sum(widths[:i]) for i in range(len(members))]
+        for member, start, width in zip(members, starts, widths):
+            emitted.append(Node(member.name, "narrow", (wide,), {"dim": 1, "start": start, "length": width},
+                                member.spec))
+            dropped.add(member.name)
+        at_leader[leader.name] = emitted
+    work = _Work(graph)
+    work.constants = constants
+    for node in graph.nodes:
+        if node.name in at_leader:
+            work.nodes.extend(at_leader[node.name])
+        elif node.name not in dropped:
+            work.nodes.append(node)
+    return work.commit(prune_constants=False)
 
-    def freed(node: Node) -> int:
-        # Bytes whose last reader is this node (outputs are never freed).
-        return sum(
-            specs[s].nbytes
-            for s in set(node.inputs)
-            if s in position and s not in outputs and pending_users.get(s, 0) == 1
-        )
 
-    ready = [n for n in graph.nodes if not waiting[n.name]]
-    order: list[Node] = []
-    while ready:
-        pick = max(ready, key=lambda n: score(n, position[n.name], freed(n)))
-        ready.remove(pick)
-        order.append(pick)
-        for user in sorted(users.get(pick.name, ())):
-            waiting[user].discard(pick.name)
-            if not waiting[user]:
-                ready.append(by_name[user])
-        for s in set(pick.inputs):
-            if s in pending_users:
-                pending_users[s] -= 1
-    if len(order) != len(graph.nodes):
-        raise GraphError("graph contains a cycle")
-    return order
+# -- scheduling --------------------------------------------------------------------------
+
+class _ListScheduler:
+    """Greedy topological ordering: repeatedly emit the ready node of highest priority.
+
+    A priority sees the node, its position in the input order and ``freed``:
+    the bytes of its inputs that no later node reads (graph outputs are never
+    freed).
+    """
+
+    def __init__(self, graph: Graph):
+        self.graph = graph
+        self.position = {n.name: i for i, n in enumerate(graph.nodes)}
+        self.specs = graph.specs()
+        self.readers_of: dict[str, list[str]] = {}
+        for node in graph.nodes:
+            for src in dict.fromkeys(node.inputs):
+                self.readers_of.setdefault(src, []).append(node.name)
+
+    def order(self, priority: Callable[[Node, int, int], tuple]) -> list[Node]:
+        graph, position, specs = self.graph, self.position, self.specs
+        by_name = {n.name: n for n in graph.nodes}
+        unmet = {n.name: len({i for i in n.inputs if i in position}) for n in graph.nodes}
+        unread = {name: len(readers) for name, readers in self.readers_of.items() if name in position}
+        outputs = set(graph.outputs)
+
+        def freed(node: Node) -> int:
+            return sum(specs[i].nbytes for i in set(node.inputs)
+                       if i in position and i not in outputs and unread.get(i) == 1)
+
+        ready = [n for n in graph.nodes if unmet[n.name] == 0]
+        emitted: list[Node] = []
+        while ready:
+            best = max(range(len(ready)), key=lambda j: priority(ready[j], position[ready[j].name], freed(ready[j])))
+            node = ready.pop(best)
+            emitted.append(node)
+            for reader in sorted(self.readers_of.get(node.name, ())):
+                unmet[reader] -= 1
+                if unmet[reader] == 0:
+                    ready.append(by_name[reader])
+            for i in set(node.inputs):
+                if i in unread:
+                    unread[i] -= 1
+        if len(emitted) != len(graph.nodes):
+            raise GraphError("graph contains a cycle")
+        return emitted
 
 
-_SCHEDULE_SCORES = (
-    lambda node, pos, freed: (freed - node.spec.nbytes, -pos),
-    lambda node, pos, freed: (freed - 2 * node.spec.nbytes, -pos),
-    lambda node, pos, freed: (freed - node.spec.nbytes // 2, -pos),
-    lambda node, pos, freed: (-node.spec.nbytes, freed, -pos),
-    lambda node, pos, freed: (-pos,),
-    lambda node, pos, freed: (pos,),
+# The six priorities tried (each ends in a unique position term, so no two
+# ready nodes tie): trade freed bytes against the bytes a node allocates at
+# three weights, allocate-smallest-first, and the input order and its reverse.
+_PRIORITIES: tuple[Callable[[Node, int, int], tuple], ...] = (
+    lambda n, pos, freed: (freed - n.spec.nbytes, -pos),
+    lambda n, pos, freed: (freed - 2 * n.spec.nbytes, -pos),
+    lambda n, pos, freed: (freed - n.spec.nbytes // 2, -pos),
+    lambda n, pos, freed: (-n.spec.nbytes, freed, -pos),
+    lambda n, pos, freed: (-pos,),
+    lambda n, pos, freed: (pos,),
 )
 
 
 def schedule(graph: Graph) -> Graph:
     """Reorder nodes for the smallest planned arena (ties: lexicographic names)."""
-    candidates: list[list[Node]] = []
-    seen: set[tuple[str, ...]] = set()
-    for score in _SCHEDULE_SCORES:
-        order = _greedy_order(graph, score)
-        names = tuple(n.name for n in order)
-        if names not in seen:
-            seen.add(names)
-            candidates.append(order)
+    scheduler = _ListScheduler(graph)
+    orders: dict[tuple[str, ...], list[Node]] = {}
+    for priority in _PRIORITIES:
+        order = scheduler.order(priority)
+        orders.setdefault(tuple(n.name for n in order), order)
 
-    def cost(order: list[Node]):
-        planned = plan_memory(_with_nodes(graph, order, dict(graph.constants))).planned_bytes
-        return planned, tuple(n.name for n in order)
+    def arena_bytes(names: tuple[str, ...]) -> int:
+        work = _Work(graph)
+        work.nodes = orders[names]
+        return plan_memory(work.commit(prune_constants=False)).planned_bytes
 
-    return _with_nodes(graph, min(candidates, key=cost), dict(graph.constants))
+    best = min(orders, key=lambda names: (arena_bytes(names), names))
+    work = _Work(graph)
+    work.nodes = orders[best]
+    return work.commit(prune_constants=False)
 
 
 PIPELINE = (
@@ -412,12 +465,13 @@ PIPELINE = (
 
 
 def optimize(graph: Graph) -> tuple[Graph, list[PassRecord]]:
+    """Run the pipeline on a copy of ``graph``; records node counts per pass."""
     graph.validate()
-    work = graph.clone()
+    current = graph.clone()
     records: list[PassRecord] = []
-    for name, fn in PIPELINE:
-        before = len(work.nodes)
-        work = fn(work)
-        work.validate()
-        records.append(PassRecord(name, before, len(work.nodes)))
-    return work, records
+    for name, run in PIPELINE:
+        before = len(current.nodes)
+        current = run(current)
+        current.validate()
+        records.append(PassRecord(name, before, len(current.nodes)))
+    return current, records
