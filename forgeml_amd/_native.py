@@ -19,7 +19,7 @@ from forgeml_amd.ir import GraphError
 LIBRARY_PATH = Path(__file__).resolve().parent / "libforgeml_hip.so"
 HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "forgeml_hip.h"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU = 0, 1, 2, 3
@@ -39,6 +39,11 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I32, _I32, _I32, _P, _I64,
          _P],
     ),
+    "forgeml_hip_gemm_noalloc": (
+        ctypes.c_int,
+        [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _I32, _I32, _P],
+    ),
+    "forgeml_hip_noalloc_scratch_bytes": (_I64, []),
     "forgeml_hip_layer_norm": (ctypes.c_int, [_P, _I64, _P, _P, _P, _I64, _I64, ctypes.c_float, _I32, _P]),
     "forgeml_hip_attention": (
         ctypes.c_int,

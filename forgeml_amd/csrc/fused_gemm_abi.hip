@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 
 #include "forgeml_hip.h"
 #include "gemm_launch.hpp"
@@ -478,3 +479,68 @@ int forgeml_hip_gemm_add(const void* a, int64_t sam, int64_t sak, const void* b,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The allocation-free entry point.  Its split-K planes live in `scratch`, a
+// file-scope device array every GPU holds a copy of from the library's first
+// use on it until the process ends.  The host-side name `scratch` is only a
+// stand-in for the symbol: the device address of this GPU's copy comes from
+// hipGetSymbolAddress, looked up once per device with that device current
+// and kept in g_scratch.  Nothing in the planes needs clearing between
+// calls: each K slice overwrites its whole M x N plane before the reduce
+// kernel reads it.
+namespace forgeml {
+
+constexpr int64_t kScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+static std::mutex g_scratch_lock;
+static void* g_scratch[kMaxDevices];
+
+static int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(FORGEML_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(FORGEML_EHIP, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(FORGEML_EHIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return FORGEML_OK;
+}
+
+}  // namespace forgeml
+
+extern "C" {
+
+int64_t forgeml_hip_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int forgeml_hip_gemm_noalloc(const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk, int64_t sbn,
+                             const void* bias, int64_t sbi, void* c, int64_t m, int64_t n, int64_t k, int32_t dtype,
+                             int32_t act, int32_t config_id, void* stream) {
+  g_last_error[0] = '\0';
+  LaunchPlan plan;
+  const int rc = plan_launch(a, sam, sak, b, sbk, sbn, m, n, k, dtype, config_id, plan);
+  if (rc != FORGEML_OK) return rc;
+  if (plan.ws_need > kScratchBytes)
+    return set_error(FORGEML_EWORKSPACE,
+                     "this shape splits K %d ways and needs %lld bytes of scratch; the allocation-free entry point "
+                     "holds %lld (use forgeml_hip_gemm with a workspace)",
+                     plan.split.splits, (long long)plan.ws_need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (plan.ws_need > 0) {
+    const int src = scratch_for_current_device(&ws);
+    if (src != FORGEML_OK) return src;
+  }
+  return gemm_impl(a, sam, sak, b, sbk, sbn, bias, sbi, c, nullptr, 0, 0, m, n, k, dtype, act, config_id, ws,
+                   plan.ws_need, stream);
+}
+
+}  // extern "C"
+

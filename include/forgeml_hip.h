@@ -115,6 +115,30 @@ int forgeml_hip_gemm_add(const void* a, int64_t sam, int64_t sak,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/*
+ * forgeml_hip_gemm without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference (its
+ * launcher has no split-K workspace).  A shape whose K is split keeps its
+ * fp32 partial planes in a scratch array the library holds on each GPU it
+ * runs on, from the first call there until the process ends, of
+ * forgeml_hip_noalloc_scratch_bytes() bytes (32 MiB); a shape that needs
+ * more is refused with FORGEML_EWORKSPACE and nothing is launched.  The
+ * call allocates nothing.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or threads) race and
+ * must be serialised by the caller.  Other arguments, errors and results
+ * are forgeml_hip_gemm's (the same kernels run).
+ */
+int forgeml_hip_gemm_noalloc(const void* a, int64_t sam, int64_t sak,
+                             const void* b, int64_t sbk, int64_t sbn,
+                             const void* bias, int64_t sbi,
+                             void* c, int64_t m, int64_t n, int64_t k,
+                             int32_t dtype, int32_t act, int32_t config_id,
+                             void* stream);
+
+/* Bytes of the per-GPU scratch array of forgeml_hip_gemm_noalloc. */
+int64_t forgeml_hip_noalloc_scratch_bytes(void);
+
 /* What forgeml_hip_gemm would run for these operands, without launching:
  *   out[0]  the config id (resolved when config_id is FORGEML_CONFIG_AUTO)
  *   out[1]  the number of K slices (1 = K is not split)
@@ -184,7 +208,7 @@ const char* forgeml_hip_last_error(void);
 /* ABI version of this header; bumped on any signature change. */
 int forgeml_hip_abi_version(void);
 
-#define FORGEML_HIP_ABI_VERSION 4
+#define FORGEML_HIP_ABI_VERSION 5
 
 #ifdef __cplusplus
 }
