@@ -11,6 +11,8 @@ Run ``python -m forgeml_amd._build`` to rebuild.
 
 from __future__ import annotations
 
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -84,7 +86,31 @@ def build(jobs: int | None = None) -> Path:
     tmp = LIBRARY.with_suffix(".so.tmp")
     _run([compiler, *HIPCC_FLAGS, "-shared", "-o", str(tmp), *map(str, objects)])
     os.replace(tmp, LIBRARY)
+    _write_build_info(sources)
     return LIBRARY
+
+
+BUILD_INFO = PACKAGE_DIR / "_build_info.json"
+
+
+def _write_build_info(sources) -> None:
+    """Provenance of the built library, read by measurement.environment where
+    the tree has no git metadata: the commit it was built at and a hash of
+    every kernel source and header it was built from."""
+    digest = hashlib.sha256()
+    for path in sorted([*sources, *CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")]):
+        digest.update(path.name.encode())
+        digest.update(path.read_bytes())
+    info = {"sources_sha256": digest.hexdigest(), "hipcc_flags": HIPCC_FLAGS}
+    try:
+        info["git_commit"] = subprocess.check_output(["git", "rev-parse", "HEAD"], cwd=REPO_ROOT, text=True,
+                                                     stderr=subprocess.DEVNULL).strip()
+        info["git_dirty"] = bool(subprocess.check_output(["git", "status", "--porcelain", "--", "forgeml_amd/csrc",
+                                                          "include"], cwd=REPO_ROOT, text=True,
+                                                         stderr=subprocess.DEVNULL).strip())
+    except (OSError, subprocess.CalledProcessError):
+        info["git_commit"] = None
+    BUILD_INFO.write_text(json.dumps(info, indent=1) + "\n")
 
 
 if __name__ == "__main__":

@@ -101,10 +101,10 @@ int launch_one(const GemmArgs& p, hipStream_t stream) {
 // (the planner refuses those requests first).
 template <int DT, int BM, int BN, int WM, int WN, int COMBO, int AMODE, int BMODE>
 int launch_combo(const GemmArgs& p, hipStream_t stream) {
-  if constexpr (combo_supported(DT == DT_F32 ? 0 : 1, BM, BN, WM * WN, COMBO))
-    return launch_one<DT, BM, BN, WM, WN, AMODE, BMODE>(p, stream);
-  else
+  if constexpr (!combo_supported(DT == DT_F32 ? 0 : 1, BM, BN, WM * WN, COMBO))
     return set_error(-2, "tile %dx%d (%d waves) is not built for operand combination %d", BM, BN, WM * WN, COMBO);
+  else
+    return launch_one<DT, BM, BN, WM, WN, AMODE, BMODE>(p, stream);
 }
 
 template <int DT, int BM, int BN, int WM, int WN>

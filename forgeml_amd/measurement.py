@@ -193,7 +193,7 @@ def check_output(actual: torch.Tensor, expected: torch.Tensor, *, rtol: float | 
 
 # -- provenance ------------------------------------------------------------------
 
-def _cpu_description() -> dict[str, Any]:
+def cpu_description() -> dict[str, Any]:
     """CPU model and core counts of this host, read from /proc/cpuinfo."""
     info: dict[str, Any] = {"cpu_model": platform.processor() or None, "logical_cpus": os.cpu_count()}
     try:
@@ -245,8 +245,15 @@ def environment(device: torch.device | str) -> dict[str, Any]:
         "timing": "synchronized_host_wall_clock",
         "percentile_method": "linear_interpolation_at_(n-1)*q",
     }
-    meta.update(_cpu_description())
+    meta.update(cpu_description())
     meta.update(_git_state(Path(__file__).resolve().parents[1]))
+    try:  # the kernel library's own record of what it was built from
+        built = json.loads((Path(__file__).resolve().parent / "_build_info.json").read_text())
+        meta["library_build"] = {k: built.get(k) for k in ("git_commit", "git_dirty", "sources_sha256")}
+        if meta.get("git_commit") is None:
+            meta["git_commit"] = built.get("git_commit")
+    except (OSError, ValueError):
+        meta["library_build"] = None
     if device.type == "cuda":
         props = torch.cuda.get_device_properties(device)
         meta.update(

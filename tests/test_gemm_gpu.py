@@ -447,3 +447,44 @@ def test_gelu_tail_contract(gpu, dtype, approximate):
         _say(what)
         got = kernels.matmul(a_d, b_d, activation="gelu", approximate=approximate).cpu()
         _contract(got, a, b, None, "gelu", approximate, what)
+
+
+# -- the 8-wave 256x256 16-bit tile at edges, K tails and split K -------------
+
+def _eight_wave_config(dtype):
+    (cfg,) = [c for c in kernels.candidates(dtype) if (c.block_m, c.block_n, c.num_waves) == (256, 256, 8)]
+    return cfg
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k", [(392, 328, 520), (256, 256, 64), (1000, 3000, 1536), (512, 512, 8192), (300, 700, 72),
+                                   (4096, 2048, 1000)])
+def test_eight_wave_tile(gpu, dtype, m, n, k):
+    """Edge tiles in M and N, K tails shorter than a stage, one-stage K, and a
+    grid small enough to split K; every epilogue, held to the contract."""
+    cfg = _eight_wave_config(dtype)
+    seed = case_seed("eight_wave", m, n, k, dtype)
+    a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout="nt")
+    a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+    info = kernels.plan(a_d, b_d, cfg)
+    acc = a.double() @ b.double()
+    for with_bias in (False, True):
+        for activation, approximate in (("none", "none"), ("gelu", "none"), ("gelu", "tanh"), ("relu", "none")):
+            what = (f"8-wave {m}x{n}x{k} {dtype} splits={info['k_splits']} bias={with_bias} "
+                    f"act={activation}/{approximate} seed={seed}")
+            _say(what)
+            bb, bb_d = (bias, bias_d) if with_bias else (None, None)
+            got = kernels.matmul(a_d, b_d, bb_d, activation=activation, approximate=approximate, config=cfg)
+            _gate(got, reference_cpu(a, b, bb, activation, approximate), k, what)
+            _contract(got, a, b, bb, activation, approximate, what, acc=acc)
+    # residual after the activation, into a fresh output and in place
+    g = torch.Generator().manual_seed(seed + 1)
+    r = torch.randn(m, n, generator=g).to(dtype)
+    expected = reference_cpu(a, b, bias, "gelu") + r
+    got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", residual=r.to(gpu), config=cfg)
+    _gate(got, expected, k, f"8-wave residual {m}x{n}x{k}")
+    out = r.to(gpu)
+    kernels.matmul(a_d, b_d, bias_d, activation="gelu", residual=out, out=out, config=cfg)
+    _gate(out, expected, k, f"8-wave residual in place {m}x{n}x{k}")
+    # deterministic
+    assert torch.equal(kernels.matmul(a_d, b_d, bias_d, config=cfg), kernels.matmul(a_d, b_d, bias_d, config=cfg))
