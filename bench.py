@@ -415,6 +415,17 @@ def block_op_workloads(steps: int, warmup: int):
         del q, k, v
 
 
+def _calibration_copy() -> None:
+    """One plain 256 MiB device copy: a dispatch of known bytes read and written,
+    against which HBM byte counters of the other dispatches are scaled."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -463,6 +474,8 @@ def main() -> int:
                                        config=config, vendor=args.vendor, **EXTRA_KW[args.only])), flush=True)
         return 0
     if args.skinny:
+        if args.calibrate_copy:
+            _calibration_copy()
         ok = True
         for shape in SKINNY_SHAPES:
             rec = skinny_workload(*shape)
@@ -470,12 +483,7 @@ def main() -> int:
             print(json.dumps(rec), flush=True)
         return 0 if ok else 1
     if args.calibrate_copy:
-        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        _calibration_copy()
     m = n = k = 4096
     head = gemm_workload("fused_addmm_bias_gelu_erf_fp32_4096", m, n, k, torch.float32,
                          steps=args.steps, warmup=args.warmup)

@@ -110,8 +110,8 @@ static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // the few-row kernel is bounded by one workgroup per 16 columns and 16 rows.
 static constexpr int64_t kMaxItems = (int64_t)1 << 32;
 static int64_t launch_items(const TileConfig& t, int64_t m, int64_t n, int64_t splits) {
-  const int64_t wgs = t.kind == KIND_SKINNY ? cdiv(n, 16) * cdiv(m, 16) : cdiv(m, t.bm) * cdiv(n, t.bn) * splits;
-  return wgs * (t.wm * t.wn * 64);
+  if (t.kind == KIND_SKINNY) return cdiv(n, 16) * cdiv(m, 16) * kSkinnyWaves * 64;
+  return cdiv(m, t.bm) * cdiv(n, t.bn) * splits * (t.wm * t.wn * 64);
 }
 
 // Load width (bytes) of the few-row kernel for these operands, or 0 when it
@@ -122,28 +122,30 @@ static int skinny_width(int64_t m, int64_t k, int64_t sam, int64_t sak, int64_t 
   if (m > kSkinnyMaxRows || sak != 1 || sbk != 1 || sam < 0 || sbn < 0 || sam >= kMaxBufferBytes ||
       sbn >= kMaxBufferBytes)
     return 0;
-  if (((m - 1) * sam + k) * esz + 16 >= kMaxBufferBytes || (15 * sbn + k) * esz + 16 >= kMaxBufferBytes) return 0;
+  // (+32: rows under 16-byte alignment round each operand's range out to 16-byte blocks)
+  if (((m - 1) * sam + k) * esz + 32 >= kMaxBufferBytes || (15 * sbn + k) * esz + 32 >= kMaxBufferBytes) return 0;
   if (ma == MODE_K && mb == MODE_K) return 16;
   if ((ma == MODE_K || ma == MODE_K4) && (mb == MODE_K || mb == MODE_K4)) return 4;
   return esz == 2 ? 2 : 0;
 }
 
 // Whether the shape heuristic prefers the few-row kernel (it runs whenever
-// skinny_width allows, if asked for by config id).  Each of its 8 waves
-// streams its share of K through a ring of kSkinnyDepth chunks, one memory
-// latency per ring round, and every workgroup (16 columns) reads all of A.
-// It beats the tiled kernels when a wave needs at most two rounds and either
-// A is at most one 16-row block (so reading it per workgroup is cheap) or,
-// with 16-byte loads, there are enough column groups to spread over the GPU;
-// at most three rounds for one row block.  Long K and narrow N go to the
-// tiled kernels (with split K).
+// skinny_width allows, if asked for by config id).  Its 8 waves per
+// workgroup stream K in chunks of 64 bytes per row, and every workgroup (16
+// columns) reads all of A.  Measured against the best tiled candidate with
+// split K (HIP graph, weights cold): it wins on every shape with up to 48 rows
+// and up to 24 chunks per wave, e.g. fp32 1x3000x4096 13.4 us against 29.3,
+// fp32 17x3000x3000 19.7 against 24.6, fp32 33x3000x1531 16.9 against 21.9,
+// as long as there are enough column groups to spread over the GPU; at 64 rows
+// only up to 8 chunks per wave (fp32 64x3000x2048: 25.2 against 23.2).  Long
+// K over few columns goes to the tiled kernels, whose split K uses every CU.
 static bool skinny_preferred(int64_t m, int64_t n, int64_t k, int lw, int esz) {
   if (lw == 0) return false;
-  const int64_t chunk = 64 / esz;  // K elements per chunk: 4 lane groups of 16 bytes
-  const int64_t per_wave = cdiv(cdiv(k, chunk), kSkinnyWaves);
-  const int64_t rounds = cdiv(per_wave, kSkinnyDepth);
-  if (m <= 16) return rounds <= 3;
-  return lw == 16 && rounds <= 2 && cdiv(n, 16) >= 48;
+  const int64_t per_wave = cdiv(cdiv(k, 64 / esz), kSkinnyWaves);  // chunks each wave streams
+  const int64_t groups = cdiv(n, 16);
+  if (m <= 16) return per_wave <= 12 || (per_wave <= 32 && groups >= 64);
+  if (m <= 48) return per_wave <= 24 && groups >= 48;
+  return per_wave <= 8 && groups >= 48;
 }
 
 static int skinny_id(int dclass) {

@@ -135,10 +135,22 @@ int launch_tile(const GemmArgs& p, int combo, hipStream_t stream) {
 // splitting a grid of 192 column groups lost 9-24 %.
 constexpr int64_t kSkinnySplitMaxWgs = 128;
 
+// Chunks in flight per few-row wave: 2 while a wave's share of K is at most
+// 6 chunks, else kSkinnyDepth.  Measured (bf16 1x3000x1531, 6 chunks per
+// wave) 5.6 us at 2 against 6.2 at 4; fp32 (12 chunks) 7.8 at 4 against 8.6.
+inline int skinny_depth(int64_t k, int esz) {
+  const int64_t chunks = (k + 64 / esz - 1) / (64 / esz);
+  return (chunks + kSkinnyWaves - 1) / kSkinnyWaves <= 6 ? 2 : kSkinnyDepth;
+}
+
 template <int DT, int TM, int LW>
 int launch_skinny_one(const GemmArgs& p, hipStream_t stream) {
   const unsigned gx = (unsigned)((p.n + 15) / 16), gy = (unsigned)((p.m + 16 * TM - 1) / (16 * TM));
-  hipLaunchKernelGGL((skinny_gemm_kernel<DT, TM, LW>), dim3(gx, gy), dim3(kSkinnyThreads), 0, stream, p);
+  if (skinny_depth(p.k, DTraits<DT>::ESZ) == 2)
+    hipLaunchKernelGGL((skinny_gemm_kernel<DT, TM, LW, 2>), dim3(gx, gy), dim3(kSkinnyWaves * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<DT, TM, LW, kSkinnyDepth>), dim3(gx, gy), dim3(kSkinnyWaves * 64), 0, stream,
+                       p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(-3, "kernel launch failed: %s", hipGetErrorString(e));
   return 0;

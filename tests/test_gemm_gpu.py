@@ -281,12 +281,14 @@ def test_split_k_workspace_is_checked(gpu):
 
 # -- the few-row kernel (M <= 64, K-contiguous A and B) -------------------------
 #
-# K values cover 16-byte rows (768, 1024), 4-byte rows (odd fp32 K 1531; 16-bit
-# K = 2 mod 8: 1002) and 2-byte rows (odd 16-bit K 1531); M covers 1..4 row
-# blocks of 16 and N edges of the 16-column workgroups.
+# K values cover 16-byte rows (768), 4-byte rows (odd fp32 K 1531; 16-bit
+# K = 2 mod 8: 1002, 2050) and 2-byte rows (odd 16-bit K 1531, 2001), and both
+# ring depths (2 chunks in flight up to 6 chunks per wave: 16-bit K <= 1536,
+# fp32 K <= 768; else 4); M covers 1..4 row blocks of 16 and N edges of the
+# 16-column workgroups.
 
 @pytest.mark.parametrize("dtype", _DTYPES)
-@pytest.mark.parametrize("k", [8, 768, 1002, 1531])
+@pytest.mark.parametrize("k", [8, 768, 1002, 1531, 2001, 2050])
 def test_few_row_kernel(gpu, dtype, k):
     config = kernels.SKINNY_FP32 if dtype == torch.float32 else kernels.SKINNY_H16
     for m in (1, 5, 16, 17, 33, 64):
@@ -301,6 +303,42 @@ def test_few_row_kernel(gpu, dtype, k):
                 _gate(got, reference_cpu(a, b, bias, activation, approximate), k, what)
             got = kernels.matmul(a_d, b_d, config=config)
             _gate(got, reference_cpu(a, b), k, f"few-row M={m} N={n} K={k} {dtype} no bias, explicit config")
+
+
+def _at_offset(t: torch.Tensor, device, elems: int) -> torch.Tensor:
+    """A copy of 2-D ``t`` on ``device`` whose storage starts ``elems`` elements
+    past an allocation (so its base is not 16-byte aligned), same strides."""
+    flat = torch.zeros(t.numel() + elems + 8, dtype=t.dtype, device=device)
+    view = flat[elems:elems + t.numel()].view(t.shape)
+    view.copy_(t.to(device))
+    return view
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_few_row_kernel_misaligned_bases(gpu, dtype):
+    """Operands whose base addresses and rows sit at every element offset of a
+    16-byte block (odd and even K), on the few-row kernel's dword-aligned
+    loads: the last row of each buffer ends inside a 16-byte block, where the
+    tail lanes realign an aligned block instead."""
+    cfg = kernels.SKINNY_FP32 if dtype == torch.float32 else kernels.SKINNY_H16
+    esz = torch.tensor([], dtype=dtype).element_size()
+    for k in (1531, 1002, 37, 2001):
+        for m, n in ((1, 3000), (5, 40), (33, 200)):
+            seed = case_seed("few_row_misaligned", m, n, k, dtype)
+            a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+            expected = reference_cpu(a, b, bias, "gelu")
+            for off_a, off_b in ((1, 3), (16 // esz - 1, 2), (2, 16 // esz - 1), (0, 1)):
+                a_d = _at_offset(a, gpu, off_a)
+                w_d = _at_offset(b.t().contiguous(), gpu, off_b)  # W [N, K] row-major; B = W^T
+                b_d = w_d.t()
+                what = f"few-row misaligned M={m} N={n} K={k} {dtype} offsets=({off_a},{off_b}) seed={seed}"
+                _say(what)
+                plan = kernels.plan(a_d, b_d, cfg)
+                assert plan["kernel"] == "few-row", plan
+                got = kernels.matmul(a_d, b_d, bias.to(gpu), activation="gelu", config=cfg)
+                _gate(got, expected, k, what)
+                if dtype != torch.float32:
+                    _contract(got, a, b, bias, "gelu", "none", what)
 
 
 def test_few_row_kernel_strided_rows_and_determinism(gpu):

@@ -133,13 +133,19 @@ def test_few_row_kernel_selection():
     skinny = [i for i, info in enumerate(table) if info[2] == 16]
     assert len(skinny) == 2 and {table[i][0] for i in skinny} == {0, 1}
     for dtype in (_native.DTYPE_F32, _native.DTYPE_BF16):
-        # Few rows, K streamed in at most two rounds per wave: the few-row kernel.
+        # Few rows and enough column groups: the few-row kernel, up to 32
+        # chunks of K per wave for one row block, 24 up to 48 rows, 8 at 64.
         assert lib.forgeml_hip_select_config(1, 3072, 1024, dtype) in skinny
         assert lib.forgeml_hip_select_config(48, 3072, 1024, dtype) in skinny
+        assert lib.forgeml_hip_select_config(1, 3000, 4096, dtype) in skinny
+        assert lib.forgeml_hip_select_config(33, 3000, 1531, dtype) in skinny
+        assert lib.forgeml_hip_select_config(17, 3000, 3000, dtype) in skinny
         # More than 64 rows, a long K, or too few column groups: the tiled kernels.
         assert lib.forgeml_hip_select_config(65, 3072, 1024, dtype) not in skinny
         assert lib.forgeml_hip_select_config(64, 4096, 4096, dtype) not in skinny
         assert lib.forgeml_hip_select_config(64, 512, 2048, dtype) not in skinny
+        assert lib.forgeml_hip_select_config(1, 256, 16384, dtype) not in skinny
+        assert lib.forgeml_hip_select_config(33, 3000, 16384, dtype) not in skinny
     # The few-row kernel needs K-contiguous A and B and at most 64 rows.
     dummy = ctypes.c_void_p(16)
     f32_skinny = next(i for i in skinny if table[i][0] == 0)
@@ -170,9 +176,9 @@ def test_gemm_plan_reports_what_runs():
     rc, (cid, splits, ws, kind) = plan(4096, 4096, 4096, 4096, 1, 1, 4096)
     assert rc == 0 and kind == 0 and splits == 1 and ws == 0
     assert cid == lib.forgeml_hip_select_config(4096, 4096, 4096, f32)
-    # Odd fp32 K and 33 rows: 4-byte rows go to the tiled kernels.
+    # Odd fp32 K and 33 rows: 4-byte rows on the few-row kernel.
     rc, (cid, splits, ws, kind) = plan(33, 3000, 1531, 1531, 1, 1, 1531)
-    assert rc == 0 and kind == 0
+    assert rc == 0 and kind == 1 and splits == 1 and ws == 0
     # Errors are the launch's errors.
     rc, _ = plan(8, 64, 64, 64, 1, -1, 1)  # negative stride
     assert rc == _native.EINVAL
