@@ -81,9 +81,17 @@ def candidates(dtype: torch.dtype) -> tuple[KernelConfig, ...]:
     return tuple(c for c, k in zip(CANDIDATES, _CANDIDATE_CLASS) if k == dclass)
 
 
+_ARCH_BY_INDEX: dict[int, str] = {}
+
+
 def _device_arch(device: torch.device) -> str:
-    props = torch.cuda.get_device_properties(device)
-    return str(getattr(props, "gcnArchName", "")).split(":")[0]
+    """gfx name of a GPU (e.g. "gfx950"), looked up once per device index."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    arch = _ARCH_BY_INDEX.get(index)
+    if arch is None:
+        props = torch.cuda.get_device_properties(index)
+        arch = _ARCH_BY_INDEX[index] = str(getattr(props, "gcnArchName", "")).split(":")[0]
+    return arch
 
 
 def _gpu_ok(device: torch.device | None = None) -> bool:
@@ -220,6 +228,7 @@ def matmul(
     config: KernelConfig = DEFAULT_CONFIG,
     out: torch.Tensor | None = None,
     residual: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """out = act(rnd(rnd(a @ b) + bias)) on the gfx950 kernels.
 
@@ -228,8 +237,13 @@ def matmul(
     the epilogue).  ``residual`` (keyword only, not in the reference's
     signature) adds an [M, N] tensor after the activation in the same
     epilogue, as the reference's following ``add`` node would; it may be
-    ``out`` itself.  Launches on ``torch.cuda.current_stream()`` of ``a``'s
-    device and returns ``out`` (allocated when None).
+    ``out`` itself.  ``workspace`` (keyword only, not in the reference's
+    signature): a uint8 GPU buffer for split-K partial sums, at least
+    ``plan(a, b, config)["workspace_bytes"]`` (or ``workspace_for``) bytes and
+    16-byte aligned; when given, no per-call plan is made and the library
+    refuses one that is too small.  Without it the call plans and allocates
+    what the split needs.  Launches on ``torch.cuda.current_stream()`` of
+    ``a``'s device and returns ``out`` (allocated when None).
     """
     if not torch.cuda.is_available():
         raise GraphError("hip matmul requires a ROCm GPU visible to torch (torch.cuda)")
@@ -292,9 +306,16 @@ def matmul(
             and (residual.data_ptr() != out.data_ptr() or residual.stride() != out.stride())
         ):
             raise GraphError("residual must be out itself or not share its storage")
+    if workspace is not None and (
+        not isinstance(workspace, torch.Tensor) or workspace.device != a.device or workspace.dtype != torch.uint8
+        or not workspace.is_contiguous()
+    ):
+        raise GraphError("workspace must be a contiguous uint8 GPU tensor on the inputs' device")
     with torch.cuda.device(a.device):
-        nbytes = plan(a, b, config)["workspace_bytes"]
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+        ws = workspace
+        if ws is None:
+            nbytes = plan(a, b, config)["workspace_bytes"]
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
         return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws,
                       residual=residual)
 
@@ -407,6 +428,14 @@ def select_kernels(graph: Graph, backend: str) -> dict[str, str]:
     return plan
 
 
+# Every kernel a compiled model can launch: the tiled fused GEMM, the few-row
+# GEMM, the split-K reduce (in gemm_kernels.hpp), and LayerNorm / attention.
+KERNEL_SOURCES = ("gemm_kernels.hpp", "skinny_kernels.hpp", "block_kernels.hip")
+
+
 def kernel_source() -> str:
-    """Source text of the HIP kernels (the reference returns its Triton source)."""
-    return importlib.resources.files("forgeml_amd").joinpath("csrc", "gemm_kernels.hpp").read_text()
+    """Source text of the HIP kernels a compiled model can run, each file
+    under a ``// ===== csrc/<name> =====`` line (the reference returns its
+    Triton module's source)."""
+    root = importlib.resources.files("forgeml_amd").joinpath("csrc")
+    return "\n".join(f"// ===== csrc/{name} =====\n{root.joinpath(name).read_text()}" for name in KERNEL_SOURCES)

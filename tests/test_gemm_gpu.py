@@ -277,6 +277,14 @@ def test_split_k_workspace_is_checked(gpu):
     ws = kernels.workspace_for(m, n, k, torch.float32, -1, gpu)
     kernels.launch(a_d, b_d, None, out, act=0, config_id=-1, workspace=ws)
     _gate(out, reference_cpu(a, b), k, "split-K explicit workspace")
+    # matmul with a caller's workspace: no per-call plan, the same result; a
+    # workspace too small is refused by the library before any launch.
+    got = kernels.matmul(a_d, b_d, workspace=ws)
+    assert torch.equal(got, out)
+    with pytest.raises(RuntimeError, match="workspace"):
+        kernels.matmul(a_d, b_d, workspace=ws[:16])
+    with pytest.raises(GraphError, match="workspace"):
+        kernels.matmul(a_d, b_d, workspace=ws.view(torch.float32))
 
 
 # -- the few-row kernel (M <= 64, K-contiguous A and B) -------------------------

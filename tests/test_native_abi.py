@@ -80,7 +80,12 @@ def test_matmul_boundary_validation_on_cpu():
     with pytest.raises(GraphError):
         kernels._check_config(kernels.candidates(torch.bfloat16)[0], torch.float32)
     assert kernels._check_config(kernels.DEFAULT_CONFIG, torch.float32) == _native.CONFIG_AUTO
-    assert "fused_gemm_kernel" in kernels.kernel_source() and "__global__" in kernels.kernel_source()
+    source = kernels.kernel_source()
+    for kernel in ("fused_gemm_kernel", "splitk_reduce_kernel", "skinny_gemm_kernel", "layer_norm_kernel",
+                   "attention_kernel", "__global__"):
+        assert kernel in source, kernel
+    for name in kernels.KERNEL_SOURCES:
+        assert f"// ===== csrc/{name} =====" in source
 
 
 def test_split_k_workspace_size():
