@@ -345,7 +345,7 @@ struct AttnArgs {
   int64_t sq[4], sk[4], sv[4], so[4];  // element strides (batch, head, sequence, dim)
   int batch, heads, lq, lk;
   int nqb;       // query blocks of 32 per (batch, head)
-  int nitems;    // work items per (batch, head): query blocks, or causal pairs of them
+  int nitems;    // work items per (batch, head): its query blocks
   int causal;
   float scale_log2;  // scale * log2(e): softmax in base 2
 };
@@ -360,13 +360,20 @@ struct AttnArgs {
 // attention at 8x12x512, -3 % causal, +3 % on a 1024-long causal problem.
 constexpr int kAttnSplit = 4;
 
-// One workgroup: one work item of head (b, h).  A work item is query block qb
-// (rows [32*qb, 32*qb + 32)); with the causal mask it is the pair of blocks t
-// and nqb-1-t, whose key blocks add up to nqb+1 for every t, so all
-// workgroups carry the same work and none waits on the longest rows alone.
+// One workgroup: one work item of head (b, h), query block qb (rows [32*qb,
+// 32*qb + 32)).  With the causal mask, workgroup g takes query block
+// nqb-1-g/(B*H): the grid lists the items longest first (qb + 1 key blocks),
+// so as workgroups finish, the dispatcher hands the free CUs ever shorter
+// items and the GPU drains evenly (longest-processing-time-first).  Measured
+// against pairing blocks t and nqb-1-t into equal items (whose count, 3/2 of
+// the workgroup slots on an 8x12x512 problem, left half the CUs idle in a
+// second round): 54.2 -> 51.8 us at 8x12x512x64, 12.2 -> 9.1 us at 2x8x333x32.
 // Two waves per SIMD up to head dim 96: at 96 that spills some registers and
 // is still faster than one wave per SIMD (76 vs 98 us on an 8x12x512 causal
-// problem).  Head dim 128 holds twice dim 64's fragments: one wave per SIMD.
+// problem).  Head dim 128 holds twice dim 64's fragments: one wave per SIMD,
+// so nothing else hides a key block's K load: that wave loads the next key
+// block's K while it works on this one (883 -> 794 us on full attention at
+// 4x32x1024x128; at dim 64 the extra registers cost what they hide).
 template <int D>
 __global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(D <= 96 ? 2 : 1, 8)))
 void attention_kernel(AttnArgs p) {
@@ -383,7 +390,6 @@ void attention_kernel(AttnArgs p) {
   const int nbh = p.batch * p.heads;
   const int t = g / nbh, bh = g % nbh;
   const int b = bh / p.heads, h = bh % p.heads;
-  const int nrep = (p.causal && t != p.nqb - 1 - t) ? 2 : 1;
   const float* qp = p.q + b * p.sq[0] + h * p.sq[1];
   const float* kp = p.k + b * p.sk[0] + h * p.sk[1];
   const float* vp = p.v + b * p.sv[0] + h * p.sv[1];
@@ -391,8 +397,7 @@ void attention_kernel(AttnArgs p) {
   const __amdgpu_buffer_rsrc_t kr = make_rsrc((const char*)kp, (uint32_t)(((int64_t)(p.lk - 1) * p.sk[2] + D) * 4));
   const __amdgpu_buffer_rsrc_t vr = make_rsrc((const char*)vp, (uint32_t)(((int64_t)(p.lk - 1) * p.sv[2] + D) * 4));
 
-  for (int rep = 0; rep < nrep; ++rep) {
-  const int qb = rep == 0 ? (p.causal ? p.nqb - 1 - t : t) : t;
+  const int qb = p.causal ? p.nqb - 1 - t : t;
   const int q0 = qb * 32;
   // Q^T operand: this lane's query row lc, dims 8c + 4*half + e.
   const int qrow = q0 + lc;
@@ -406,13 +411,25 @@ void attention_kernel(AttnArgs p) {
   const int last_key = p.causal ? min(p.lk, q0 + 32) : p.lk;  // keys [0, last_key) can be visible
   const int nkb = (last_key + 31) / 32;
 
+  // Loads of a key block: a lane's offset within the block is the same for
+  // every block, and the block's own offset is wave-uniform, so it rides in
+  // the loads' scalar offset and the loop spends no vector instructions on
+  // addresses.  Only the block holding the end of the keys (a uniform test)
+  // checks keys lane by lane (past the end: out of range, read as zeros).
+  const uint32_t k_lane = (uint32_t)(((int64_t)lc * p.sk[2] + 4 * half) * 4);
+  const uint32_t v_lane = (uint32_t)(((int64_t)4 * half * p.sv[2] + lc) * 4);
   auto load_k = [&](int kb, u32x4 (&kf)[NC]) {
-    const int key = kb * 32 + lc;
+    if (kb >= nkb) return;  // a prefetch past this wave's last block
+    const int blk = (int)((int64_t)kb * 32 * p.sk[2] * 4);
+    if (kb * 32 + 32 <= p.lk) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const uint32_t off =
-          (kb < nkb && key < p.lk) ? (uint32_t)(((int64_t)key * p.sk[2] + 8 * c + 4 * half) * 4) : kOutOfRange;
-      kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)off, 0, 0));
+      for (int c = 0; c < NC; ++c)
+        kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(k_lane + 32 * c), blk, 0));
+    } else {
+      const uint32_t o = kb * 32 + lc < p.lk ? k_lane + (uint32_t)blk : kOutOfRange;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(o + 32 * c), 0, 0));
     }
   };
 
@@ -425,25 +442,36 @@ void attention_kernel(AttnArgs p) {
 
   // V^T operand of a key block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
   auto load_v = [&](int kb, float (&vf)[NB][16]) {
+    if (kb * 32 + 32 <= p.lk) {
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const int key = kb * 32 + 8 * (s >> 2) + 4 * half + (s & 3);
+      for (int s = 0; s < 16; ++s) {
+        const int blk = (int)((int64_t)(kb * 32 + 8 * (s >> 2) + (s & 3)) * p.sv[2] * 4);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint32_t off =
-            (kb < nkb && key < p.lk) ? (uint32_t)(((int64_t)key * p.sv[2] + lc + 32 * nb) * 4) : kOutOfRange;
-        vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)off, 0, 0));
+        for (int nb = 0; nb < NB; ++nb)
+          vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb), blk, 0));
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int row = kb * 32 + 8 * (s >> 2) + (s & 3);  // the key of half 0
+        const uint32_t o =
+            row + 4 * half < p.lk ? v_lane + (uint32_t)((int64_t)row * p.sv[2] * 4) : kOutOfRange;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(o + 128 * nb), 0, 0));
       }
     }
   };
 
-  // K and V of a key block load at its start; V is needed only after S and
-  // the softmax.  Two waves per SIMD (the registers of a next-block prefetch
-  // would allow one) hide the K latency better than a prefetch does.
+  // V of a key block loads at its start: it is needed only after S and the
+  // softmax.  K loads at the start too, where two waves per SIMD hide its
+  // latency; at head dim 128 it is prefetched a key block ahead.
+  constexpr bool k_ahead = D == 128;
+  u32x4 kf[NC];
+  if constexpr (k_ahead) load_k(wave, kf);
   for (int kb = wave; kb < nkb; kb += kAttnSplit) {
-    u32x4 kf[NC];
+    if constexpr (!k_ahead) load_k(kb, kf);
     float vf[NB][16];
-    load_k(kb, kf);
     load_v(kb, vf);
 
     // S^T[key][query] for this block, as two independent MFMA chains (even
@@ -457,6 +485,7 @@ void attention_kernel(AttnArgs p) {
         s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c + 1][e]), __uint_as_float(qf[c + 1][e]), s1, 0,
                                                   0, 0);
       }
+    if constexpr (k_ahead) load_k(kb + kAttnSplit, kf);  // out of range past this wave's last block
 
     // Online softmax for query qrow (this lane's column), keys of this half.
     // Key blocks entirely visible to every query of the block skip the mask.
@@ -475,11 +504,13 @@ void attention_kernel(AttnArgs p) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m, mx);
     const float base = m_new == -INFINITY ? 0.0f : m_new;  // rows with nothing visible yet
-    const float alpha = exp2f(m - base);
+    // v_exp_f32 directly: results under 2^-126 (flushed) are below a
+    // rounding error of a sum that holds a 1.
+    const float alpha = __builtin_amdgcn_exp2f(m - base);
     float rs = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[i] = exp2f(s[i] - base);
+      s[i] = __builtin_amdgcn_exp2f(s[i] - base);
       rs += s[i];
     }
     rs += __shfl_xor(rs, 32, 64);
@@ -555,9 +586,6 @@ void attention_kernel(AttnArgs p) {
         dst[3 * p.so[3]] = val.w;
       }
     }
-  }
-  // The next query block reuses tr and part after these reads.
-  __syncthreads();
   }
 }
 
@@ -645,7 +673,7 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
   p.lq = (int)lq;
   p.lk = (int)lk;
   p.nqb = (int)nqb;
-  p.nitems = causal ? (int)((nqb + 1) / 2) : (int)nqb;
+  p.nitems = (int)nqb;
   p.causal = causal != 0;
   p.scale_log2 = scale * 1.44269504088896340736f;
   switch (dim) {
