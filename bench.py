@@ -373,18 +373,32 @@ ATTN_CASES = [(8, 12, 512, 64, True), (8, 12, 512, 128, True), (4, 32, 1024, 128
 
 def block_op_workloads(steps: int, warmup: int):
     """The transformer block's LayerNorm and attention kernels against torch's
-    GPU kernels for the same ops, per-launch HIP-event µs (median), one record
-    per case.  LayerNorm also reports its HBM floor (read x, write y at 8 TB/s)."""
+    GPU kernels for the same ops, one record per case.  ``us`` is the GPU time
+    per launch over ``steps`` back-to-back launches (HIP events around the
+    block, after at least 10 warmup launches: the first launches of a long
+    kernel run while the clock ramps); ``us_per_launch_median`` the median of
+    events recorded between the launches (each adds a few µs of gap).  Ours
+    and torch's are timed the same way.  LayerNorm also reports its HBM floor
+    (read x, write y at 8 TB/s)."""
     import torch.nn.functional as F
 
     from forgeml_amd import kernels
+    from forgeml_amd.measurement import event_times
 
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev).manual_seed(0)
 
     def med_us(fn):
-        _, per = _time_launches(fn, steps, warmup)
-        return round(statistics.median(per) * 1e3, 2)
+        """(block mean, per-launch median) in µs."""
+        per = event_times(fn, iters=steps, warmup=max(warmup, 10))
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        stream.synchronize()
+        return round(start.elapsed_time(end) * 1e3 / steps, 2), round(statistics.median(per) * 1e3, 2)
 
     for rows, cols, dt in LN_SHAPES:
         x = torch.randn(rows, cols, device=dev, generator=g).to(dt)
@@ -395,10 +409,11 @@ def block_op_workloads(steps: int, warmup: int):
         tol = 1e-4 if dt == torch.float32 else 2.0 ** -7
         gate = {"passed": bool(((got - want).abs() <= tol * (1 + want.abs())).all()),
                 "max_abs_err": float((got - want).abs().max())}
-        ours = med_us(lambda: kernels.layer_norm(x, (cols,), w, b, 1e-5))
-        ref = med_us(lambda: F.layer_norm(x, (cols,), w, b, 1e-5))
+        ours, ours_med = med_us(lambda: kernels.layer_norm(x, (cols,), w, b, 1e-5))
+        ref, ref_med = med_us(lambda: F.layer_norm(x, (cols,), w, b, 1e-5))
         floor = 2 * x.numel() * x.element_size() / (HBM_GBPS * 1e3)
         yield {"workload": f"layer_norm_{DTYPE_NAMES[dt]}_{rows}x{cols}", "us": ours, "torch_gpu_us": ref,
+               "us_per_launch_median": ours_med, "torch_gpu_us_per_launch_median": ref_med,
                "hbm_floor_us": round(floor, 2), "hbm_frac": round(floor / ours, 3), "gate": gate}
         del x, w, b
     for bsz, heads, seq, dim, causal in ATTN_CASES:
@@ -407,11 +422,12 @@ def block_op_workloads(steps: int, warmup: int):
         want = F.scaled_dot_product_attention(q.cpu(), k.cpu(), v.cpu(), is_causal=causal)
         gate = {"passed": bool(((got - want).abs() <= 1e-5 + 1e-4 * want.abs()).all()),
                 "max_abs_err": float((got - want).abs().max())}
-        ours = med_us(lambda: kernels.attention(q, k, v, is_causal=causal))
-        ref = med_us(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal))
+        ours, ours_med = med_us(lambda: kernels.attention(q, k, v, is_causal=causal))
+        ref, ref_med = med_us(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal))
         flop = 4 * bsz * heads * seq * seq * dim * (0.5 if causal else 1.0)
         yield {"workload": f"attention_fp32_{bsz}x{heads}x{seq}x{dim}_{'causal' if causal else 'full'}", "us": ours,
-               "torch_gpu_us": ref, "tflops": round(flop / ours / 1e6, 1), "gate": gate}
+               "torch_gpu_us": ref, "us_per_launch_median": ours_med, "torch_gpu_us_per_launch_median": ref_med,
+               "tflops": round(flop / ours / 1e6, 1), "gate": gate}
         del q, k, v
 
 

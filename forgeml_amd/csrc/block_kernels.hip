@@ -350,15 +350,20 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e): softmax in base 2
 };
 
-// Four waves share a work item: wave w takes the item's key blocks kb with
-// kb % 4 == w and keeps its own online-softmax state (m, l, O); waves 1-3
-// hand their states to wave 0 through LDS, which merges, normalises and
-// transposes the output, and all four store it.  The split multiplies the
-// waves in flight (one work item per wave left a quarter of the SIMDs idle
-// on a transformer block's heads) and shortens each wave's serial chain of
-// key blocks.  Measured against two waves per item: -17 % on full
-// attention at 8x12x512, -3 % causal, +3 % on a 1024-long causal problem.
-constexpr int kAttnSplit = 4;
+// kAttnSplit (2 or 4) waves share a work item: wave w takes the item's key
+// blocks kb with kb % kAttnSplit == w and keeps its own online-softmax state
+// (m, l, O); the others hand their states to wave 0 through LDS, which
+// merges, normalises and transposes the output, and all of them store it.
+// The split multiplies the waves in flight and shortens each wave's serial
+// chain of key blocks; two waves give each wave a longer pipelined chain and
+// half the merging.  Measured (us, four waves -> two): head dim 128: 8x12x512
+// causal 115 -> 86, 4x32x1024 causal 444 -> 353, full 688 -> 608; head dim
+// 96 causal 67 -> 61; head dim 64: 8x12x512 causal 49.8 -> 45.6, 4x16x1024
+// causal 91.9 -> 90.9, but full 8x12x512 66 -> 77 and 2x8x333 (dim 32)
+// causal 7.7 -> 10.6.  attention_split() holds the rule.
+inline int attention_split(int64_t items, int64_t dim, bool causal) {
+  return dim >= 96 || (causal && items >= 1024) ? 2 : 4;
+}
 
 // One workgroup: one work item of head (b, h), query block qb (rows [32*qb,
 // 32*qb + 32)).  With the causal mask, workgroup g takes query block
@@ -374,7 +379,7 @@ constexpr int kAttnSplit = 4;
 // so nothing else hides a key block's K load: that wave loads the next key
 // block's K while it works on this one (883 -> 794 us on full attention at
 // 4x32x1024x128; at dim 64 the extra registers cost what they hide).
-template <int D>
+template <int D, int kAttnSplit>
 __global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(D <= 96 ? 2 : 1, 8)))
 void attention_kernel(AttnArgs p) {
   static_assert(D % 32 == 0 && D <= 128, "head dim must be 32, 64, 96 or 128");
@@ -414,23 +419,15 @@ void attention_kernel(AttnArgs p) {
   // Loads of a key block: a lane's offset within the block is the same for
   // every block, and the block's own offset is wave-uniform, so it rides in
   // the loads' scalar offset and the loop spends no vector instructions on
-  // addresses.  Only the block holding the end of the keys (a uniform test)
-  // checks keys lane by lane (past the end: out of range, read as zeros).
+  // addresses.  Keys past lk are past the resources' ends (rows are at least
+  // D elements apart): they read as zeros.
   const uint32_t k_lane = (uint32_t)(((int64_t)lc * p.sk[2] + 4 * half) * 4);
   const uint32_t v_lane = (uint32_t)(((int64_t)4 * half * p.sv[2] + lc) * 4);
   auto load_k = [&](int kb, u32x4 (&kf)[NC]) {
-    if (kb >= nkb) return;  // a prefetch past this wave's last block
     const int blk = (int)((int64_t)kb * 32 * p.sk[2] * 4);
-    if (kb * 32 + 32 <= p.lk) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(k_lane + 32 * c), blk, 0));
-    } else {
-      const uint32_t o = kb * 32 + lc < p.lk ? k_lane + (uint32_t)blk : kOutOfRange;
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(o + 32 * c), 0, 0));
-    }
+    for (int c = 0; c < NC; ++c)
+      kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(k_lane + 32 * c), blk, 0));
   };
 
   f32x16 o[NB];
@@ -442,59 +439,35 @@ void attention_kernel(AttnArgs p) {
 
   // V^T operand of a key block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
   auto load_v = [&](int kb, float (&vf)[NB][16]) {
-    if (kb * 32 + 32 <= p.lk) {
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int blk = (int)((int64_t)(kb * 32 + 8 * (s >> 2) + (s & 3)) * p.sv[2] * 4);
+    for (int s = 0; s < 16; ++s) {
+      const int blk = (int)((int64_t)(kb * 32 + 8 * (s >> 2) + (s & 3)) * p.sv[2] * 4);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb), blk, 0));
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int row = kb * 32 + 8 * (s >> 2) + (s & 3);  // the key of half 0
-        const uint32_t o =
-            row + 4 * half < p.lk ? v_lane + (uint32_t)((int64_t)row * p.sv[2] * 4) : kOutOfRange;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(o + 128 * nb), 0, 0));
-      }
+      for (int nb = 0; nb < NB; ++nb)
+        vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb), blk, 0));
     }
   };
 
-  // V of a key block loads at its start: it is needed only after S and the
-  // softmax.  K loads at the start too, where two waves per SIMD hide its
-  // latency; at head dim 128 it is prefetched a key block ahead.
-  constexpr bool k_ahead = D == 128;
-  u32x4 kf[NC];
-  if constexpr (k_ahead) load_k(wave, kf);
-  for (int kb = wave; kb < nkb; kb += kAttnSplit) {
-    if constexpr (!k_ahead) load_k(kb, kf);
-    float vf[NB][16];
-    load_v(kb, vf);
-
-    // S^T[key][query] for this block, as two independent MFMA chains (even
-    // and odd dim chunks) so consecutive MFMAs do not wait on each other.
-    f32x16 s = {}, s1 = {};
+  // S^T[key][query] of the block in kf: one chain of dependent MFMAs, summed
+  // over the head dim in order (two chains, even and odd dim chunks, cost 16
+  // more VGPRs and an add per score, and measured no faster).
+  auto scores = [&](const u32x4 (&kf)[NC], f32x16& s) {
+    s = f32x16{};
 #pragma unroll
-    for (int c = 0; c < NC; c += 2)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 4; ++e)
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c][e]), __uint_as_float(qf[c][e]), s, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(kf[c + 1][e]), __uint_as_float(qf[c + 1][e]), s1, 0,
-                                                  0, 0);
-      }
-    if constexpr (k_ahead) load_k(kb + kAttnSplit, kf);  // out of range past this wave's last block
-
-    // Online softmax for query qrow (this lane's column), keys of this half.
-    // Key blocks entirely visible to every query of the block skip the mask.
+  };
+  // Online softmax for query qrow (this lane's column) over block kb's keys of
+  // this half: P into s; m, l and O^T rescaled.  Only the item's last key
+  // block can hold keys that are masked (causal diagonal, or past the end).
+  auto softmax = [&](int kb, f32x16& s, bool masked) {
     float mx = -INFINITY;
-    const bool full = kb * 32 + 32 <= p.lk && (!p.causal || kb * 32 + 31 <= q0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float x = (s[i] + s1[i]) * p.scale_log2;
-      if (!full) {
+      float x = s[i] * p.scale_log2;
+      if (masked) {
         const int key = kb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
         x = (key < p.lk && (!p.causal || key <= qrow)) ? x : -INFINITY;
       }
@@ -520,14 +493,46 @@ void attention_kernel(AttnArgs p) {
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[nb][i] *= alpha;
-
-    // O^T[dim][query] += V^T[dim][key] P^T[key][query]: step i takes the key of
-    // this lane's accumulator value i.
+  };
+  // O^T[dim][query] += V^T[dim][key] P^T[key][query]: step i takes the key of
+  // this lane's accumulator value i.
+  auto accumulate = [&](const float (&vf)[NB][16], const f32x16& s) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[nb][i], s[i], o[nb], 0, 0, 0);
+  };
 
+  // This wave's key blocks kb_j = wave + kAttnSplit*j, j < n, software
+  // pipelined: iteration j issues the S MFMAs of block j+1, then the softmax
+  // of block j (VALU work the SIMD runs while the matrix pipe is busy), block
+  // j's PV MFMAs, and the loads of K of block j+2 and V of block j+1 behind
+  // them.  Keys past the end read as zeros (the resources end at key lk, and
+  // rows are at least D apart) and are masked in the last block's softmax.
+  const int n = wave < nkb ? (nkb - 1 - wave) / kAttnSplit + 1 : 0;
+  const int kb_last = wave + kAttnSplit * (n - 1);
+  u32x4 kf[NC];
+  float vf[NB][16];
+  f32x16 s;
+  if (n > 0) {
+    load_k(wave, kf);
+    load_v(wave, vf);
+    scores(kf, s);
+    load_k(min(wave + kAttnSplit, kb_last), kf);
+  }
+  for (int j = 0; j + 1 < n; ++j) {
+    const int kb = wave + kAttnSplit * j;
+    f32x16 sn;
+    scores(kf, sn);
+    load_k(min(kb + 2 * kAttnSplit, kb_last), kf);
+    softmax(kb, s, false);
+    accumulate(vf, s);
+    load_v(kb + kAttnSplit, vf);
+    s = sn;
+  }
+  if (n > 0) {
+    softmax(kb_last, s, kb_last == nkb - 1);
+    accumulate(vf, s);
   }
 
   // Merge the waves' states (base-2 running max m, sum l, unnormalised O^T):
@@ -592,7 +597,10 @@ void attention_kernel(AttnArgs p) {
 template <int D>
 static int launch_attention(const AttnArgs& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.batch * p.heads * p.nitems;
-  hipLaunchKernelGGL((attention_kernel<D>), dim3((unsigned)items), dim3(kAttnSplit * 64), 0, stream, p);
+  if (attention_split(items, D, p.causal) == 2)
+    hipLaunchKernelGGL((attention_kernel<D, 2>), dim3((unsigned)items), dim3(2 * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attention_kernel<D, 4>), dim3((unsigned)items), dim3(4 * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FORGEML_EHIP, "attention launch failed: %s", hipGetErrorString(e));
   return FORGEML_OK;
@@ -648,13 +656,18 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
   if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || (sq[2] % 4) || (sk[2] % 4) || (sq[0] % 4) || (sq[1] % 4) ||
       (sk[0] % 4) || (sk[1] % 4))
     return set_error(FORGEML_EINVAL, "attention: q and k rows must be 16-byte aligned");
-  // 32-bit byte offsets within one (batch, head) slice.
-  if (((lq - 1) * sq[2] + dim) * 4 >= ((int64_t)1 << 31) || ((lk - 1) * sk[2] + dim) * 4 >= ((int64_t)1 << 31) ||
-      ((lk - 1) * sv[2] + dim) * 4 >= ((int64_t)1 << 31))
+  // K and V rows at least a head dim apart: keys past the end (in the last
+  // 32-key block) then fall outside the buffer resources, which end at key lk.
+  if (sk[2] < dim || sv[2] < dim)
+    return set_error(FORGEML_EINVAL, "attention: k and v rows must be at least the head dim apart");
+  // 32-bit byte offsets within one (batch, head) slice, up to the end of the
+  // last 32-key block.
+  if (((lq - 1) * sq[2] + dim) * 4 >= ((int64_t)1 << 31) || ((lk + 31) * sk[2] + dim) * 4 >= ((int64_t)1 << 31) ||
+      ((lk + 31) * sv[2] + dim) * 4 >= ((int64_t)1 << 31))
     return set_error(FORGEML_EINVAL, "attention: a (batch, head) slice exceeds 2 GiB");
   const int64_t nqb = (lq + 31) / 32;
   // One workgroup per work item: the dispatch must cover fewer than 2^32 work-items.
-  if (batch * heads * nqb * (kAttnSplit * 64) >= ((int64_t)1 << 32))
+  if (batch * heads * nqb * (4 * 64) >= ((int64_t)1 << 32))
     return set_error(FORGEML_EINVAL, "attention: more than 2^24 query blocks in one call");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(FORGEML_EINVAL, "attention: scale must be finite and positive");
   AttnArgs p;

@@ -384,9 +384,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, is_causal: b
         raise GraphError(f"hip attention shapes {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)} not supported")
     qkv = []
     for t in (q, k, v):
-        if t.stride(3) != 1 or t.data_ptr() % 16 or any(s % 4 for s in t.stride()[:3]):
-            # A fresh allocation: contiguous() would hand back a contiguous
-            # tensor whose storage offset leaves it misaligned.
+        if t.stride(3) != 1 or t.stride(2) < dim or t.data_ptr() % 16 or any(s % 4 for s in t.stride()[:3]):
+            # The kernel reads rows of D contiguous, 16-byte aligned floats at
+            # least D apart (a broadcast sequence dimension is not).  A fresh
+            # allocation: contiguous() would hand back a contiguous tensor
+            # whose storage offset leaves it misaligned.
             t = t.clone(memory_format=torch.contiguous_format)
         qkv.append(t)
     out = torch.empty(bsz, lq, heads, dim, dtype=q.dtype, device=q.device).transpose(1, 2)

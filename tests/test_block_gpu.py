@@ -81,10 +81,14 @@ def _attention_inputs(b, h, lq, lk, d, seed):
     return q, k, v
 
 
+# Two waves per work item at head dim 96 and 128, and for causal problems of
+# at least 1024 query blocks (2x32x512 at dim 64, 8x8x512 at dim 32); four
+# otherwise.
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("b,h,lq,lk,d", [(2, 3, 100, 100, 64), (1, 2, 33, 33, 32), (2, 2, 64, 64, 96),
                                           (1, 4, 512, 512, 64), (2, 1, 40, 70, 64), (1, 1, 1, 1, 64),
-                                          (2, 3, 100, 100, 128), (1, 2, 300, 300, 128)])
+                                          (2, 3, 100, 100, 128), (1, 2, 300, 300, 128), (2, 32, 512, 512, 64),
+                                          (8, 8, 512, 512, 32), (1, 2, 70, 40, 96)])
 def test_attention(gpu, causal, b, h, lq, lk, d):
     seed = case_seed("attn", b, h, lq, lk, d, causal)
     q, k, v = _attention_inputs(b, h, lq, lk, d, seed)
@@ -128,6 +132,18 @@ def test_attention_misaligned_contiguous_inputs(gpu):
     _say("attention misaligned contiguous inputs")
     got = kernels.attention(shifted(q), shifted(k), shifted(v), is_causal=True)
     expected = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-5)
+
+
+def test_attention_broadcast_keys(gpu):
+    # K and V broadcast along the sequence (stride 0): rows that overlap are
+    # copied out by the boundary before the kernel runs.
+    b, h, s, d = 2, 3, 50, 64
+    q, k, v = _attention_inputs(b, h, s, 1, d, case_seed("attn_bcast"))
+    kx, vx = k.expand(b, h, s, d), v.expand(b, h, s, d)
+    _say("attention broadcast keys")
+    got = kernels.attention(q.to(gpu), k.to(gpu).expand(b, h, s, d), v.to(gpu).expand(b, h, s, d), is_causal=True)
+    expected = F.scaled_dot_product_attention(q, kx, vx, is_causal=True)
     torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-5)
 
 

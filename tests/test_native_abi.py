@@ -204,6 +204,11 @@ def test_block_kernel_argument_errors():
     assert lib.forgeml_hip_attention(*args, 1, 1, 64, 64, 48, 1, 0.125, f32, None) == _native.EINVAL
     assert "head dim" in _native.last_error()
     assert lib.forgeml_hip_attention(*args, 1, 1, 64, 64, 64, 1, 0.125, _native.DTYPE_F16, None) == _native.EINVAL
+    # k and v rows closer than the head dim (overlapping rows) are refused
+    close = (ctypes.c_int64 * 4)(4096, 64 * 64, 32, 1)
+    assert lib.forgeml_hip_attention(dummy, st, dummy, close, dummy, st, dummy, st, 1, 1, 64, 64, 64, 1, 0.125, f32,
+                                     None) == _native.EINVAL
+    assert "apart" in _native.last_error()
     bad = (ctypes.c_int64 * 4)(4096, 64 * 64, 64, 2)
     assert lib.forgeml_hip_attention(dummy, bad, dummy, st, dummy, st, dummy, st, 1, 1, 64, 64, 64, 1, 0.125, f32,
                                      None) == _native.EINVAL
