@@ -201,57 +201,72 @@ __global__ __launch_bounds__(NT) void layer_norm_row_kernel(LnArgs p) {
   }
 }
 
+// Chan, Golub and LeVeque's merge of two partial (count, mean, M2 = sum of
+// squared deviations) statistics into (n, mean, m2).
+__device__ __forceinline__ void chan_merge(float& n, float& mean, float& m2, float nb, float mb, float m2b) {
+  const float nn = n + nb;
+  if (nn == 0.0f) return;
+  const float delta = mb - mean;
+  const float r = nb / nn;
+  mean = fmaf(delta, r, mean);
+  m2 = m2 + m2b + delta * delta * n * r;
+  n = nn;
+}
+
 // Rows wider still: one workgroup of 1024 threads per row, 16-byte vectors,
-// the row read three times (the re-reads mostly from cache).
+// the row read twice.  The first pass folds each vector's own mean and
+// squared deviations into the thread's running (count, mean, M2) by Chan's
+// merge, then merges lanes and waves the same way (waves in order): the
+// centred variance without a separate pass for the mean (512x200000 fp32:
+// 334 -> 274 us against three passes).  The second pass normalises.
 constexpr int kLnWideThreads = 1024;
 template <int DT>
 __global__ __launch_bounds__(kLnWideThreads) void layer_norm_wide_kernel(LnArgs p) {
   constexpr int ESZ = DTraits<DT>::ESZ;
   constexpr int VEC = 16 / ESZ;
   constexpr int NT = kLnWideThreads, NW = NT / 64;
-  __shared__ float part_s[NW], part_q[NW];
+  __shared__ float part[3][NW];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int row = blockIdx.x;  // one row per workgroup: every thread reaches the barriers
+  const int row = blockIdx.x;  // one row per workgroup: every thread reaches the barrier
   const char* xr = p.x + (int64_t)row * p.sx * ESZ;
-  float sum = 0.0f;
+  float n = 0.0f, mean = 0.0f, m2 = 0.0f;
 #pragma unroll 4
-  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
+  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {  // rows hold whole vectors
     float v[VEC];
     unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
+    float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) sum += v[e];
-  }
-  sum = wave_sum(sum);
-  if (lane == 0) part_s[wave] = sum;
-  __syncthreads();
-  float total = 0.0f;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) total += part_s[w];
-  const float mean = total / (float)p.cols;
-  float sq = 0.0f;
-#pragma unroll 4
-  for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
-    float v[VEC];
-    unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
+    for (int e = 0; e < VEC; ++e) s += v[e];
+    const float mb = s * (1.0f / VEC);
+    float q = 0.0f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float d = v[e] - mean;
-      sq += d * d;
+      const float d = v[e] - mb;
+      q = fmaf(d, d, q);
     }
+    chan_merge(n, mean, m2, (float)VEC, mb, q);
   }
-  sq = wave_sum(sq);
-  if (lane == 0) part_q[wave] = sq;
-  __syncthreads();
-  float totq = 0.0f;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) totq += part_q[w];
-  const float rstd = 1.0f / sqrtf(totq / (float)p.cols + p.eps);
+  for (int off = 32; off > 0; off >>= 1) {
+    const float nb = __shfl_xor(n, off, 64), mb = __shfl_xor(mean, off, 64), qb = __shfl_xor(m2, off, 64);
+    chan_merge(n, mean, m2, nb, mb, qb);
+  }
+  if (lane == 0) {
+    part[0][wave] = n;
+    part[1][wave] = mean;
+    part[2][wave] = m2;
+  }
+  __syncthreads();
+  float tn = part[0][0], tm = part[1][0], tq = part[2][0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) chan_merge(tn, tm, tq, part[0][w], part[1][w], part[2][w]);
+  const float rstd = 1.0f / sqrtf(tq / (float)p.cols + p.eps);
   char* yr = p.y + (int64_t)row * p.cols * ESZ;
 #pragma unroll 4
   for (int64_t c0 = (int64_t)t * VEC; c0 < p.cols; c0 += NT * VEC) {
     float v[VEC];
     unpack16<DT>(*(const u32x4*)(xr + c0 * ESZ), v);
-    ln_store_vec<DT>(p, yr, c0, v, mean, rstd);
+    ln_store_vec<DT>(p, yr, c0, v, tm, rstd);
   }
 }
 
