@@ -273,7 +273,8 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
     return FORGEML_OK;
   }
   out[3] = t.dclass == 0 ? kRowBytes / 4 : kRowBytes / 2;
-  // Stages and LDS as built for K-contiguous operands (transposing loaders use two stages).
+  // Stages and LDS at most, for K-contiguous operands (transposing loaders use
+  // two stages, and a 64x64 tile runs two on grids of more than 512 workgroups).
   const int stages = (int64_t)t.bm * t.bn <= 64 * 64 ? 4 : 2;
   out[5] = stages;
   out[6] = (int32_t)kMaxSplit;

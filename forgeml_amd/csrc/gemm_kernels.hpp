@@ -527,11 +527,12 @@ struct LoaderG {
   }
 };
 
-// LDS stage buffers of a kernel: small tiles whose operands both arrive by
-// DMA stream K with little MFMA work per stage, so they keep four stages in
-// flight (64 KiB, two workgroups per CU); the others use two.
+// Most LDS stage buffers a kernel may ring through: small tiles whose
+// operands both arrive by DMA stream K with little MFMA work per stage, so
+// they can keep four stages in flight (64 KiB, two workgroups per CU); the
+// others use two.  The launcher picks the ring per grid (launch_one).
 template <int BM, int BN, int AMODE, int BMODE>
-constexpr int lds_stages() {
+constexpr int lds_stages_max() {
   return ((AMODE == MODE_K || AMODE == MODE_K4) && (BMODE == MODE_K || BMODE == MODE_K4) && BM * BN <= 64 * 64) ? 4
                                                                                                               : 2;
 }
@@ -843,7 +844,7 @@ struct Occupancy {
   static constexpr int WAVES = ACC_REGS >= 128 ? 1 : ((ACC_REGS >= 64 || REG_STAGED) ? 2 : 4);
 };
 
-template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
+template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE, int S>
 __global__ __launch_bounds__(WM* WN * 64)
 __attribute__((amdgpu_waves_per_eu(Occupancy<DT, BM, BN, WM, WN, AMODE, BMODE>::WAVES, 8)))
 void fused_gemm_kernel(GemmArgs p) {
@@ -892,8 +893,8 @@ void fused_gemm_kernel(GemmArgs p) {
   constexpr int NG_DIRECT = (LA::kDirect ? LA::kGlobalLoads : 0) + (LB::kDirect ? LB::kGlobalLoads : 0);
   constexpr int NG_REG = (LA::kDirect ? 0 : LA::kGlobalLoads) + (LB::kDirect ? 0 : LB::kGlobalLoads);
   constexpr int NW = LA::kLdsWrites + LB::kLdsWrites;
-  constexpr int S = lds_stages<BM, BN, AMODE, BMODE>();
-  static_assert(S == 2 || (LA::kDirect && LB::kDirect && LA::kExactPer && LB::kExactPer),
+  static_assert(S == 2 || (S <= lds_stages_max<BM, BN, AMODE, BMODE>() && LA::kDirect && LB::kDirect &&
+                            LA::kExactPer && LB::kExactPer),
                 "rings deeper than two stages count DMA instructions per wave exactly");
   using Fr = Frags<FTM, FTN>;
   // 16x16x32 path: per-lane offsets of the two steps' chunks (rows 16 apart

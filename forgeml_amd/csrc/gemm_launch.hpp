@@ -71,11 +71,11 @@ int launch_reduce(const GemmArgs& p, hipStream_t stream) {
   return 0;
 }
 
-template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
-int launch_one(const GemmArgs& p, hipStream_t stream) {
+template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE, int S>
+int launch_ring(const GemmArgs& p, hipStream_t stream) {
   constexpr int NT = WM * WN * 64;
-  constexpr int LDS = lds_stages<BM, BN, AMODE, BMODE>() * (BM + BN) * kRowBytes;
-  const void* fn = reinterpret_cast<const void*>(&fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE>);
+  constexpr int LDS = S * (BM + BN) * kRowBytes;
+  const void* fn = reinterpret_cast<const void*>(&fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE, S>);
   if constexpr (LDS > 65536) {
     // Above 64 KiB the dynamic LDS limit must be raised once per device
     // (gfx950 has 160 KiB of LDS per CU).
@@ -90,11 +90,31 @@ int launch_one(const GemmArgs& p, hipStream_t stream) {
       ready[dev].store(1, std::memory_order_release);
     }
   }
-  hipLaunchKernelGGL((fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE>),
+  hipLaunchKernelGGL((fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE, S>),
                      dim3((unsigned)(p.tiles_m * p.tiles_n * p.splits)), dim3(NT), LDS, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(-3, "kernel launch failed: %s", hipGetErrorString(e));
   return p.splits > 1 ? launch_reduce<DT>(p, stream) : 0;
+}
+
+// A tile that may ring through four LDS stages does so while the grid holds
+// at most two workgroups per CU (MI355X: 256 CUs): then latency within a
+// workgroup is what limits it.  Larger grids take two stages (32 KiB for a
+// 64x64 tile), so up to five workgroups share a CU and hide each other's
+// prologue and epilogue.  Measured 64x64 (us, four stages -> two): fp32
+// 4096x2304x768 124.0 -> 114.9, 4096x768x3072 160.1 -> 148.4, bf16
+// 1000x3072x1024 17.2 -> 14.0; bf16 512x4096x4096 (512 workgroups) 27.8 ->
+// 33.1, 1024^3 (256) 7.9 -> 8.1.
+constexpr int64_t kDeepRingMaxWgs = 2 * 256;
+
+template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
+int launch_one(const GemmArgs& p, hipStream_t stream) {
+  constexpr int SMAX = lds_stages_max<BM, BN, AMODE, BMODE>();
+  if constexpr (SMAX > 2) {
+    if ((int64_t)p.tiles_m * p.tiles_n * p.splits <= kDeepRingMaxWgs)
+      return launch_ring<DT, BM, BN, WM, WN, AMODE, BMODE, SMAX>(p, stream);
+  }
+  return launch_ring<DT, BM, BN, WM, WN, AMODE, BMODE, 2>(p, stream);
 }
 
 // One combination of a tile, or an error when the tile is not built for it

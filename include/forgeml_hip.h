@@ -58,9 +58,10 @@ extern "C" {
 #define FORGEML_CONFIG_INFO_FIELDS 8
 /* [0] dtype class: 0 = fp32, 1 = 16-bit (bf16 and fp16)
  * [1] block_m   [2] block_n   [3] block_k (elements per LDS stage)
- * [4] waves per workgroup     [5] LDS stages
+ * [4] waves per workgroup     [5] LDS stages (at most: a launch may ring
+ *     through fewer, as the grid size and operand layout decide)
  * [6] split_k (1 = none; >1 = K split over workgroups, needs a workspace)
- * [7] LDS bytes per workgroup */
+ * [7] LDS bytes per workgroup (at the most stages) */
 
 /*
  * Fused GEMM + bias + activation.  Replaces `launch` in

@@ -287,6 +287,30 @@ def test_split_k_workspace_is_checked(gpu):
         kernels.matmul(a_d, b_d, workspace=ws.view(torch.float32))
 
 
+# -- the 64x64 tile's two LDS rings ----------------------------------------------
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_small_tile_rings(gpu, dtype):
+    """The 64x64 tile rings through four LDS stages on grids of at most 512
+    workgroups and two on larger ones, for 16-byte and 4-byte K-contiguous rows."""
+    cfg = next(c for c in kernels.candidates(dtype) if (c.block_m, c.block_n) == (64, 64))
+    odd_k = 1025 if dtype == torch.float32 else 1026  # 4-byte rows
+    for m, n, k in ((1000, 3072, 1024), (1000, 3072, odd_k), (200, 640, 1024), (200, 640, odd_k)):
+        seed = case_seed("rings", m, n, k, dtype)
+        a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+        a_d, b_d, bias_d = a.to(gpu), to_gpu(b, gpu), bias.to(gpu)
+        info = kernels.plan(a_d, b_d, cfg)
+        wgs = -(-m // 64) * -(-n // 64) * info["k_splits"]
+        what = f"64x64 M={m} N={n} K={k} {dtype} workgroups={wgs} seed={seed}"
+        _say(what)
+        got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=cfg)
+        rows = _row_sample(m, 96, seed)
+        expected = reference_cpu(a[rows], b, bias, "gelu")
+        _gate(got.cpu()[rows], expected, k, what)
+        if dtype != torch.float32:
+            _contract(got.cpu()[rows], a[rows], b, bias, "gelu", "none", what)
+
+
 # -- the few-row kernel (M <= 64, K-contiguous A and B) -------------------------
 #
 # K values cover 16-byte rows (768), 4-byte rows (odd fp32 K 1531; 16-bit
