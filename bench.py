@@ -216,6 +216,23 @@ SKINNY_SHAPES = [(m, n, k, dt) for dt in (torch.float32, torch.bfloat16) for m i
                  for n, k in ((3072, 1024), (3000, 1531))]
 
 
+# Before a latency measurement on the GPU, its variants run back to back for
+# this long: the GPU leaves its idle clocks over tens of milliseconds (a
+# transformer block measured 623 us per call over its first 20 synchronized
+# calls, then 545), and the CPU baseline before it leaves the GPU idle.
+GPU_WARMUP_S = 0.3
+
+
+@torch.inference_mode()
+def _gpu_warm(fns) -> None:
+    fns = list(fns)
+    t_end = time.perf_counter() + GPU_WARMUP_S
+    while time.perf_counter() < t_end:
+        for fn in fns:
+            fn()
+        torch.cuda.synchronize()
+
+
 def compiled_workload(name, make_model, make_input, *, steps, warmup, cpu_budget_s=20.0):
     """CompiledModel forward latency (synchronized host wall clock, as the reference
     times it): eager hip backend, the same captured in a HIP graph, and the
@@ -255,12 +272,13 @@ def compiled_workload(name, make_model, make_input, *, steps, warmup, cpu_budget
         gate[label] = bool(torch.isfinite(got).all()) and bool((err <= atol + rtol * expected.double().abs()).all())
         gate[f"{label}_max_abs_err"] = float(err.max())
     gate["passed"] = gate["hip"] and gate["hip_graph"]
-    timings = measure_variants({"hip": lambda: compiled(x), "hip_graph": lambda: graphed(x),
-                                "torch_eager_gpu": lambda: model(x)}, device=dev,
-                               warmup=warmup, repeats=max(steps, 2))
+    variants = {"hip": lambda: compiled(x), "hip_graph": lambda: graphed(x), "torch_eager_gpu": lambda: model(x)}
+    _gpu_warm(variants.values())
+    timings = measure_variants(variants, device=dev, warmup=warmup, repeats=max(steps, 2))
     # The reference's numerically gated autotuner (CompiledModel.autotune), then a new graph.
     compiled.autotune(x, warmup=2, repeats=5)
     tuned_graph = compiled.capture_graph(x)
+    _gpu_warm([lambda: tuned_graph(x)])
     tuned = measure_variants({"hip_tuned_graph": lambda: tuned_graph(x)}, device=dev, warmup=warmup,
                              repeats=max(steps, 2))["hip_tuned_graph"]
     cpu_ms = statistics.median(cpu)
@@ -278,6 +296,7 @@ def compiled_workload(name, make_model, make_input, *, steps, warmup, cpu_budget
         "gate": gate,
         "tuned_configs": {node: f"{c.block_m}x{c.block_n}x{c.num_waves}" for node, c in compiled.kernel_configs.items()},
         "fused_residual_adds": len(compiled.fused_residuals),
+        "gpu_warmup_s": GPU_WARMUP_S,
         "cpu_reference_median_us": round(cpu_ms * 1e3, 1),
         "cpu_reference_threads": torch.get_num_threads(),
         "cpu_reference_samples": len(cpu),
