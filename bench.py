@@ -450,6 +450,41 @@ def block_op_workloads(steps: int, warmup: int):
         del q, k, v
 
 
+# The transformer block's GEMMs (d = 768, 8 x 512 tokens, FFN 3072) on the
+# tiles its autotuner picks, QKV also on 128x128, and the fp32 headline.
+BLOCK_GEMMS = [("qkv_4096x2304x768", 4096, 2304, 768, "none", (64, 64, 4)),
+               ("qkv_4096x2304x768", 4096, 2304, 768, "none", (128, 128, 4)),
+               ("ffn_up_4096x3072x768_gelu", 4096, 3072, 768, "gelu", (128, 128, 4)),
+               ("ffn_down_4096x768x3072", 4096, 768, 3072, "none", (64, 64, 4)),
+               ("out_proj_4096x768x768", 4096, 768, 768, "none", (64, 64, 4)),
+               ("headline_4096x4096x4096_gelu", 4096, 4096, 4096, "gelu", (256, 128, 8))]
+
+
+def block_gemm_launches(steps: int):
+    """Each BLOCK_GEMMS case gated on sampled rows, then launched ``steps`` times
+    back to back (fp32, B = W^T, bias, the activation shown): a fixed sequence
+    of dispatches for counter runs, one record per case."""
+    from forgeml_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    for name, m, n, k, act, tile in BLOCK_GEMMS:
+        a, b, bias = _inputs(m, n, k, torch.float32, dev, seed=m + n + k)
+        cfg = next(c for c in kernels.candidates(torch.float32) if (c.block_m, c.block_n, c.num_waves) == tile)
+        out = kernels.matmul(a, b, bias, activation=act, config=cfg)
+        torch.cuda.synchronize()
+        gate = _gate_gemm(out, a, b, bias, act)
+        cid = kernels.config_id(cfg, torch.float32)
+        plan = kernels.plan(a, b, cfg)
+        ws = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev) if plan["workspace_bytes"] else None
+        code = kernels._act_code(act, "none")
+        for _ in range(steps):
+            kernels.launch(a, b, bias, out, act=code, config_id=cid, workspace=ws)
+        torch.cuda.synchronize()
+        yield {"workload": name, "shape": [m, n, k], "tile": list(tile), "kernel": plan["kernel"],
+               "k_splits": plan["k_splits"], "launches": steps, "gate": gate}
+        del a, b, bias, out
+
+
 def _calibration_copy() -> None:
     """One plain 256 MiB device copy: a dispatch of known bytes read and written,
     against which HBM byte counters of the other dispatches are scaled."""
@@ -478,6 +513,9 @@ def main() -> int:
                     help="time the LayerNorm and attention kernels against torch's GPU kernels instead")
     ap.add_argument("--skinny", action="store_true",
                     help="run only the skinny (HBM-bound) GEMM records, one JSON line each (for counter runs)")
+    ap.add_argument("--block-gemms", action="store_true",
+                    help="launch the transformer block's four fp32 GEMM shapes (and the headline) --steps times each "
+                         "on fixed tiles, one JSON line each (for counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -508,6 +546,14 @@ def main() -> int:
         print(json.dumps(gemm_workload(args.only, *EXTRA_GEMMS[args.only], steps=args.steps, warmup=args.warmup,
                                        config=config, vendor=args.vendor, **EXTRA_KW[args.only])), flush=True)
         return 0
+    if args.block_gemms:
+        if args.calibrate_copy:
+            _calibration_copy()
+        ok = True
+        for rec in block_gemm_launches(args.steps):
+            ok = ok and rec["gate"]["passed"]
+            print(json.dumps(rec), flush=True)
+        return 0 if ok else 1
     if args.skinny:
         if args.calibrate_copy:
             _calibration_copy()
