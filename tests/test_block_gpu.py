@@ -154,3 +154,22 @@ def test_block_kernel_argument_checks(gpu):
         kernels.attention(*(torch.randn(1, 1, 8, 48, device=gpu),) * 3)
     with pytest.raises(GraphError, match="does not end"):
         kernels.layer_norm(torch.randn(4, 8, device=gpu), (16,))
+
+
+def test_attention_random_problems(gpu):
+    """60 seeded random attention problems: batch and heads 1..4, lengths 1..300
+    (L_q and L_k independent), every head dim, causal or not, against torch's
+    CPU SDPA."""
+    g = torch.Generator().manual_seed(case_seed("attn_random"))
+    for i in range(60):
+        b, h = (int(v) for v in torch.randint(1, 5, (2,), generator=g))
+        lq, lk = (int(v) for v in torch.randint(1, 301, (2,), generator=g))
+        d = (32, 64, 96, 128)[int(torch.randint(0, 4, (1,), generator=g))]
+        causal = bool(torch.randint(0, 2, (1,), generator=g))
+        seed = case_seed("attn_random", i)
+        q, k, v = _attention_inputs(b, h, lq, lk, d, seed)
+        _say("attention random", i, b, h, lq, lk, d, causal, seed)
+        expected = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        got = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal)
+        torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-5,
+                                   msg=lambda msg: f"attention random #{i} {b}x{h}x{lq}x{lk}x{d} causal={causal}: {msg}")

@@ -558,3 +558,33 @@ def test_eight_wave_tile(gpu, dtype, m, n, k):
     _gate(out, expected, k, f"8-wave residual in place {m}x{n}x{k}")
     # deterministic
     assert torch.equal(kernels.matmul(a_d, b_d, bias_d, config=cfg), kernels.matmul(a_d, b_d, bias_d, config=cfg))
+
+
+# -- seeded random problems through the few-row kernel ----------------------------
+
+def test_few_row_kernel_random_problems(gpu):
+    """200 seeded random problems on the few-row kernel: M in 1..64, N in 1..300,
+    K in 1..2600, every dtype, operand bases at random element offsets, every
+    epilogue; against the CPU path (and the contract for 16-bit outputs)."""
+    g = torch.Generator().manual_seed(case_seed("few_row_random"))
+    acts = (("gelu", "none"), ("gelu", "tanh"), ("none", "none"), ("relu", "none"))
+    for i in range(200):
+        m = int(torch.randint(1, 65, (1,), generator=g))
+        n = int(torch.randint(1, 301, (1,), generator=g))
+        k = int(torch.randint(1, 2601, (1,), generator=g))
+        dtype = _DTYPES[int(torch.randint(0, 3, (1,), generator=g))]
+        activation, approximate = acts[int(torch.randint(0, 4, (1,), generator=g))]
+        off_a, off_b = (int(v) for v in torch.randint(0, 8, (2,), generator=g))
+        seed = case_seed("few_row_random", i)
+        a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed)
+        cfg = kernels.SKINNY_FP32 if dtype == torch.float32 else kernels.SKINNY_H16
+        a_d = _at_offset(a, gpu, off_a)
+        b_d = _at_offset(b.t().contiguous(), gpu, off_b).t()
+        what = (f"few-row random #{i} M={m} N={n} K={k} {dtype} {activation}/{approximate} "
+                f"offsets=({off_a},{off_b}) seed={seed}")
+        _say(what)
+        assert kernels.plan(a_d, b_d, cfg)["kernel"] == "few-row", what
+        got = kernels.matmul(a_d, b_d, bias.to(gpu), activation=activation, approximate=approximate, config=cfg)
+        _gate(got, reference_cpu(a, b, bias, activation, approximate), k, what)
+        if dtype != torch.float32:
+            _contract(got.cpu(), a, b, bias, activation, approximate, what)
