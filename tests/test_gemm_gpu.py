@@ -588,3 +588,36 @@ def test_few_row_kernel_random_problems(gpu):
         _gate(got, reference_cpu(a, b, bias, activation, approximate), k, what)
         if dtype != torch.float32:
             _contract(got.cpu(), a, b, bias, activation, approximate, what)
+
+
+def test_tiled_kernels_random_problems(gpu):
+    """120 seeded random problems on a random built tile: M, N in 1..2000, K in
+    1..3000, every dtype, B as W^T or stored [K, N], A row-major or transposed,
+    every epilogue; checked on sampled rows (a tile the layout does not build
+    must be refused with ECONFIG)."""
+    g = torch.Generator().manual_seed(case_seed("tiled_random"))
+    acts = (("gelu", "none"), ("gelu", "tanh"), ("none", "none"), ("relu", "none"))
+    for i in range(120):
+        m, n = (int(v) for v in torch.randint(1, 2001, (2,), generator=g))
+        k = int(torch.randint(1, 3001, (1,), generator=g))
+        dtype = _DTYPES[int(torch.randint(0, 3, (1,), generator=g))]
+        tiles = [c for c in kernels.candidates(dtype) if c.block_n != 16]
+        cfg = tiles[int(torch.randint(0, len(tiles), (1,), generator=g))]
+        layout = ("nt", "nn")[int(torch.randint(0, 2, (1,), generator=g))]
+        a_t = bool(torch.randint(0, 2, (1,), generator=g))
+        activation, approximate = acts[int(torch.randint(0, 4, (1,), generator=g))]
+        seed = case_seed("tiled_random", i)
+        a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout=layout)
+        a_d = a.t().contiguous().to(gpu).t() if a_t else a.to(gpu)
+        b_d = to_gpu(b, gpu)
+        what = (f"tiled random #{i} M={m} N={n} K={k} {dtype} tile={cfg.block_m}x{cfg.block_n}x{cfg.num_waves} "
+                f"B={layout} A^T={a_t} {activation}/{approximate} seed={seed}")
+        _say(what)
+        if not _built_for(a_d, b_d, cfg):
+            continue
+        got = kernels.matmul(a_d, b_d, bias.to(gpu), activation=activation, approximate=approximate, config=cfg)
+        rows = _row_sample(m, min(m, 48), seed) if m > 2 else torch.arange(m)
+        expected = reference_cpu(a[rows], b, bias, activation, approximate)
+        _gate(got.cpu()[rows], expected, k, what)
+        if dtype != torch.float32:
+            _contract(got.cpu()[rows], a[rows], b, bias, activation, approximate, what)
