@@ -265,7 +265,8 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
   out[4] = t.wm * t.wn;
   if (t.kind == KIND_SKINNY) {
     // block_k: K of one chunk (a 16-byte vector per lane, 4 lane groups);
-    // stages: chunks in flight per wave; LDS: the cross-wave reduction.
+    // stages: the most chunks in flight per wave (a launch may keep 2, as
+    // skinny_depth decides); LDS: the cross-wave reduction.
     out[3] = t.dclass == 0 ? 16 : 32;
     out[5] = kSkinnyDepth;
     out[6] = 1;

@@ -56,8 +56,8 @@ DEFAULT_CONFIG = KernelConfig()
 _FP32_TILES = ((128, 128, 4, 2), (64, 64, 4, 4), (256, 128, 8, 2))
 _H16_TILES = ((256, 256, 4, 2), (128, 128, 4, 2), (64, 64, 4, 4), (256, 256, 8, 2))
 # The few-row kernels come last: up to 64 rows, 16 columns per workgroup, 8
-# waves splitting K in chunks of 16 fp32 / 32 16-bit elements, 4 chunks in
-# flight per wave.  They run only K-contiguous A and B.
+# waves splitting K in chunks of 16 fp32 / 32 16-bit elements, up to 4 chunks
+# in flight per wave.  They run only K-contiguous A and B.
 SKINNY_FP32 = KernelConfig(64, 16, 16, 8, 4)
 SKINNY_H16 = KernelConfig(64, 16, 32, 8, 4)
 CANDIDATES: tuple[KernelConfig, ...] = tuple(
