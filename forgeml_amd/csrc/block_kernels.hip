@@ -13,9 +13,9 @@
 // fixed order, y = (x - mean) / sqrt(var + eps) * w + b in
 // fp32, rounded once to the output dtype.
 //
-// Attention (fp32, head dim D of 32, 64, 96 or 128): flash-style, four waves per
-// 32 query rows, each streaming every fourth 32-key block with an online
-// softmax, their states merged at the end.  A wave computes S^T = K Q^T on
+// Attention (fp32, head dim D of 32, 64, 96 or 128): flash-style, two or four
+// waves per 32 query rows, each streaming every second or fourth 32-key block
+// with an online softmax, their states merged at the end.  A wave computes S^T = K Q^T on
 // v_mfma_f32_32x32x2_f32, so that each lane
 // owns one query column of S^T: the softmax row statistics are a reduction
 // over the lane's 16 accumulator values plus one exchange with the other half
@@ -394,7 +394,9 @@ inline int attention_split(int64_t items, int64_t dim, bool causal) {
 // so nothing else hides a key block's K load: that wave loads the next key
 // block's K while it works on this one (883 -> 794 us on full attention at
 // 4x32x1024x128; at dim 64 the extra registers cost what they hide).
-template <int D, int kAttnSplit>
+// kShort: lk < 32, one key block, whose V rows go in the loads' vector
+// offsets (see load_v).
+template <int D, int kAttnSplit, bool kShort>
 __global__ __launch_bounds__(kAttnSplit * 64) __attribute__((amdgpu_waves_per_eu(D <= 96 ? 2 : 1, 8)))
 void attention_kernel(AttnArgs p) {
   static_assert(D % 32 == 0 && D <= 128, "head dim must be 32, 64, 96 or 128");
@@ -434,12 +436,18 @@ void attention_kernel(AttnArgs p) {
   // Loads of a key block: a lane's offset within the block is the same for
   // every block, and the block's own offset is wave-uniform, so it rides in
   // the loads' scalar offset and the loop spends no vector instructions on
-  // addresses.  Keys past lk are past the resources' ends (rows are at least
-  // D elements apart): they read as zeros.
+  // addresses.  The buffer range check covers the vector offset only, not
+  // the scalar one, so no block may reach past key lk through its scalar
+  // offset: the last block, when lk is not a multiple of 32, starts at key
+  // lk - 32 instead (its first keys, already counted by the block before,
+  // are masked in the softmax).  With lk < 32 the one block starts at key 0,
+  // its scalar offset is 0, and keys past lk fall past the resources' ends
+  // (rows are at least D elements apart): they read as zeros.
   const uint32_t k_lane = (uint32_t)(((int64_t)lc * p.sk[2] + 4 * half) * 4);
   const uint32_t v_lane = (uint32_t)(((int64_t)4 * half * p.sv[2] + lc) * 4);
+  auto key0 = [&](int kb) { return kb * 32 + 32 > p.lk && p.lk >= 32 ? p.lk - 32 : kb * 32; };
   auto load_k = [&](int kb, u32x4 (&kf)[NC]) {
-    const int blk = (int)((int64_t)kb * 32 * p.sk[2] * 4);
+    const int blk = (int)((int64_t)key0(kb) * p.sk[2] * 4);
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)(k_lane + 32 * c), blk, 0));
@@ -453,13 +461,18 @@ void attention_kernel(AttnArgs p) {
   float m = -INFINITY, l = 0.0f;
 
   // V^T operand of a key block: dim lc + 32*nb, key 8*(s/4) + 4*half + s%4.
+  // A lane's V rows vary with s, and so does the scalar offset: with lk < 32
+  // the row offset goes in the vector offset instead, where the range check
+  // zeros the rows past lk.
   auto load_v = [&](int kb, float (&vf)[NB][16]) {
+    const int k0 = key0(kb);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const int blk = (int)((int64_t)(kb * 32 + 8 * (s >> 2) + (s & 3)) * p.sv[2] * 4);
+      const int blk = (int)((int64_t)(k0 + 8 * (s >> 2) + (s & 3)) * p.sv[2] * 4);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
-        vf[nb][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb), blk, 0));
+        vf[nb][s] = __uint_as_float(kShort ? __builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb + blk), 0, 0)
+                                           : __builtin_amdgcn_raw_buffer_load_b32(vr, (int)(v_lane + 128 * nb), blk, 0));
     }
   };
 
@@ -476,15 +489,17 @@ void attention_kernel(AttnArgs p) {
   };
   // Online softmax for query qrow (this lane's column) over block kb's keys of
   // this half: P into s; m, l and O^T rescaled.  Only the item's last key
-  // block can hold keys that are masked (causal diagonal, or past the end).
+  // block can hold keys that are masked (causal diagonal, keys past the end,
+  // or, in a block moved back to start at key lk - 32, keys below kb * 32).
   auto softmax = [&](int kb, f32x16& s, bool masked) {
     float mx = -INFINITY;
+    const int k0 = key0(kb);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float x = s[i] * p.scale_log2;
       if (masked) {
-        const int key = kb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-        x = (key < p.lk && (!p.causal || key <= qrow)) ? x : -INFINITY;
+        const int key = k0 + 8 * (i >> 2) + 4 * half + (i & 3);
+        x = (key >= kb * 32 && key < p.lk && (!p.causal || key <= qrow)) ? x : -INFINITY;
       }
       s[i] = x;
       mx = fmaxf(mx, x);
@@ -612,10 +627,12 @@ void attention_kernel(AttnArgs p) {
 template <int D>
 static int launch_attention(const AttnArgs& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.batch * p.heads * p.nitems;
-  if (attention_split(items, D, p.causal) == 2)
-    hipLaunchKernelGGL((attention_kernel<D, 2>), dim3((unsigned)items), dim3(2 * 64), 0, stream, p);
+  if (p.lk < 32)
+    hipLaunchKernelGGL((attention_kernel<D, 2, true>), dim3((unsigned)items), dim3(2 * 64), 0, stream, p);
+  else if (attention_split(items, D, p.causal) == 2)
+    hipLaunchKernelGGL((attention_kernel<D, 2, false>), dim3((unsigned)items), dim3(2 * 64), 0, stream, p);
   else
-    hipLaunchKernelGGL((attention_kernel<D, 4>), dim3((unsigned)items), dim3(4 * 64), 0, stream, p);
+    hipLaunchKernelGGL((attention_kernel<D, 4, false>), dim3((unsigned)items), dim3(4 * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FORGEML_EHIP, "attention launch failed: %s", hipGetErrorString(e));
   return FORGEML_OK;
@@ -671,8 +688,8 @@ int forgeml_hip_attention(const void* q, const int64_t* sq, const void* k, const
   if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || (sq[2] % 4) || (sk[2] % 4) || (sq[0] % 4) || (sq[1] % 4) ||
       (sk[0] % 4) || (sk[1] % 4))
     return set_error(FORGEML_EINVAL, "attention: q and k rows must be 16-byte aligned");
-  // K and V rows at least a head dim apart: keys past the end (in the last
-  // 32-key block) then fall outside the buffer resources, which end at key lk.
+  // K and V rows at least a head dim apart: the last key block's resources
+  // end at key lk's row, and keys past lk then start past that end.
   if (sk[2] < dim || sv[2] < dim)
     return set_error(FORGEML_EINVAL, "attention: k and v rows must be at least the head dim apart");
   // 32-bit byte offsets within one (batch, head) slice, up to the end of the

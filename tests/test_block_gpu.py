@@ -147,6 +147,26 @@ def test_attention_broadcast_keys(gpu):
     torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("lk,d", [(70, 64), (45, 128), (33, 32), (100, 96), (20, 64), (1, 32), (31, 128)])
+def test_attention_keys_past_the_end_are_not_read(gpu, causal, lk, d):
+    # K and V are views of the first lk rows of buffers whose rows past lk
+    # hold NaN: a kernel that read a key past lk (the last 32-key block runs
+    # over it when lk is not a multiple of 32) would put a NaN into O, even
+    # with that key masked, through 0 * NaN in P V.  lk < 32: one key block.
+    b, h, lq = 2, 3, 77
+    q, k, v = _attention_inputs(b, h, lq, lk, d, case_seed("attn_tail", lk, d, causal))
+    def padded(t):
+        buf = torch.full((b, h, lk + 32, d), float("nan"), device=gpu)
+        buf[:, :, :lk] = t.to(gpu)
+        return buf[:, :, :lk]
+    _say("attention keys past the end", lk, d, causal)
+    got = kernels.attention(q.to(gpu), padded(k), padded(v), is_causal=causal)
+    expected = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+    assert not got.isnan().any()
+    torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-5)
+
+
 def test_block_kernel_argument_checks(gpu):
     with pytest.raises(GraphError, match="fp32"):
         kernels.attention(*(torch.randn(1, 1, 8, 64, device=gpu, dtype=torch.bfloat16),) * 3)
