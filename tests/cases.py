@@ -1,8 +1,7 @@
-"""Seeded inputs for the parity tests (shared by tests, smoke and bench)."""
+"""Seeded inputs for the parity tests."""
 
 from __future__ import annotations
 
-import math
 import zlib
 
 import torch
@@ -37,11 +36,3 @@ def to_gpu(t, device):
     if t.dim() == 2 and not t.is_contiguous() and t.t().is_contiguous():
         return t.t().contiguous().to(device).t()
     return t.to(device)
-
-
-def flops(m: int, n: int, k: int) -> int:
-    return 2 * m * n * k
-
-
-def sqrt(x: float) -> float:
-    return math.sqrt(x)
