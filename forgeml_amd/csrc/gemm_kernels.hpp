@@ -810,7 +810,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
 #pragma unroll
               for (int j = 0; j < 4; ++j) w[j] = pack2<DT>(v[2 * j], v[2 * j + 1]);
             }
-            *(u32x4*)dst = w;
+            // Non-temporal store: the tile is written out, not kept in
+            // L2 for a re-read (bf16 4096^3 3 % faster, bf16 4096x2304x768
+            // 10 %, fp32 up to 2 %, never slower beyond noise).
+            __builtin_nontemporal_store(w, (u32x4*)dst);
           } else {
 #pragma unroll
             for (int j = 0; j < EPV; ++j)
