@@ -11,15 +11,16 @@
 //    padded to 16 for v_mfma_f32_16x16x4_f32 (fp32) or
 //    v_mfma_f32_16x16x32_{bf16,f16} (16-bit), instead of to a 64-row tile,
 //    and split over workgroups when the column groups alone leave CUs idle.
-//  * Its 8 waves split K.  Each wave streams its K range in chunks of one
+//  * Its 8 waves split K into 8 ranges (rotated over the waves from one
+//    workgroup to the next).  Each wave streams its K range in chunks of one
 //    16-byte vector per lane per operand (16 fp32 or 32 bf16 of K), straight
 //    from global memory into registers, with D = 2 or 4 chunks in flight: no
 //    LDS staging, and every weight byte is read once.
 //  * Lane l holds column (or row) l%16 and K group l/16 of a chunk.  For fp32
 //    the 4 values of a lane's vector feed 4 MFMAs (K elements 4g+e, e = 0..3),
 //    the same permutation of K for A and B, so the sum is unchanged.
-//  * The 8 partial sums are added in LDS in wave order (deterministic), then
-//    rounded, biased, activated and stored.
+//  * The 8 partial sums are added in LDS in K-range order (deterministic),
+//    then rounded, biased, activated and stored.
 //  * Rows past M, columns past N and K past the end are out of range of the
 //    buffer resources: loads return zeros without touching memory.
 //  * Rows that are not 16-byte aligned (an odd K) still load 16-byte
@@ -202,10 +203,16 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(GemmArgs
   const int m0 = blockIdx.y * 16 * TM;
   const int j = lane & 15, kq = lane >> 4;
 
-  // This wave's chunks [c0, c1) of the K dimension.
+  // This wave's K range: chunks [c0, c1), range `slot` of WV.  The ranges
+  // rotate over the waves from one workgroup of an XCD to the next (an XCD
+  // runs every eighth workgroup index), so the workgroups side by side on an
+  // XCD start on different parts of A, which all of them read in full (1-3 %
+  // faster).  The partial sums are added in range order, whichever wave holds
+  // a range, so results do not depend on the rotation.
   const int nk = (p.k + CK - 1) / CK;
   const int per = (nk + WV - 1) / WV;
-  const int c0 = wave * per;
+  const int slot = (wave + (int)(blockIdx.x >> 3) + (int)blockIdx.y) % WV;
+  const int c0 = slot * per;
   const int c1 = min(nk, c0 + per);
 
   const uint32_t a_span = (uint32_t)(((int64_t)(p.m - 1) * p.sam + p.k) * ESZ);
@@ -274,10 +281,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(GemmArgs
     }
   }
 
-  // Partial sums of the WV waves, added in wave order.  Lane l of a 16x16
-  // accumulator holds column l%16, rows 4*(l/16) + r.
+  // Partial sums of the WV K ranges, added in range order.  Lane l of a
+  // 16x16 accumulator holds column l%16, rows 4*(l/16) + r.
 #pragma unroll
-  for (int mt = 0; mt < TM; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int mt = 0; mt < TM; ++mt) red[slot][mt][lane] = acc[mt];
   __syncthreads();
   for (int o = threadIdx.x; o < TM * 256; o += WV * 64) {
     const int mt = o >> 8, i = (o >> 4) & 15, jj = o & 15;
