@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import ctypes
 import importlib.resources
-from dataclasses import dataclass, fields
+from dataclasses import dataclass
 
 import torch
 
@@ -43,7 +43,8 @@ class KernelConfig:
 
     @property
     def is_auto(self) -> bool:
-        return all(getattr(self, f.name) is None for f in fields(self))
+        return (self.block_m is None and self.block_n is None and self.block_k is None and self.num_waves is None
+                and self.num_stages is None)
 
 
 DEFAULT_CONFIG = KernelConfig()
@@ -83,16 +84,39 @@ def candidates(dtype: torch.dtype) -> tuple[KernelConfig, ...]:
 
 
 _ARCH_BY_INDEX: dict[int, str] = {}
+_CUDA_SEEN = False  # torch.cuda.is_available() has returned True in this process
 
 
-def _device_arch(device: torch.device) -> str:
-    """gfx name of a GPU (e.g. "gfx950"), looked up once per device index."""
-    index = device.index if device.index is not None else torch.cuda.current_device()
+def _cuda_ready() -> bool:
+    """torch.cuda.is_available(), asked until it first returns True (it reads the environment each call)."""
+    global _CUDA_SEEN
+    if not _CUDA_SEEN:
+        _CUDA_SEEN = torch.cuda.is_available()
+    return _CUDA_SEEN
+
+
+def _arch_of_index(index: int) -> str:
     arch = _ARCH_BY_INDEX.get(index)
     if arch is None:
         props = torch.cuda.get_device_properties(index)
         arch = _ARCH_BY_INDEX[index] = str(getattr(props, "gcnArchName", "")).split(":")[0]
     return arch
+
+
+def _device_arch(device: torch.device) -> str:
+    """gfx name of a GPU (e.g. "gfx950"), looked up once per device index."""
+    return _arch_of_index(device.index if device.index is not None else torch.cuda.current_device())
+
+
+# hipStream_t of torch's current stream on a GPU: torch's raw-stream query
+# where the build has it (one call, no Stream object), else the public API.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(index: int) -> int:
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def _gpu_ok(device: torch.device | None = None) -> bool:
@@ -120,10 +144,11 @@ def _check_config(config: KernelConfig, dtype: torch.dtype) -> int:
         raise GraphError(f"config must be a KernelConfig, got {type(config).__name__}")
     if config.is_auto:
         return _native.CONFIG_AUTO
-    built = candidates(dtype)
-    if config not in built:
+    cid = _CONFIG_IDS.get(config)
+    if cid is None or _CANDIDATE_CLASS[cid] != (0 if dtype == torch.float32 else 1):
+        built = candidates(dtype)
         raise GraphError(f"config {config} is not a built MI355X tile for {dtype}; choose one of {list(built)}")
-    return _CONFIG_IDS[config]
+    return cid
 
 
 def config_id(config: KernelConfig, dtype: torch.dtype) -> int:
@@ -168,7 +193,7 @@ def launch(
     dtype = _DTYPE_CODES[a.dtype]
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
     if stream is None:
-        stream = torch.cuda.current_stream(a.device).cuda_stream
+        stream = _stream_handle(a.get_device())
     bias_ptr, sbi = (None, 0) if bias is None else (bias.data_ptr(), bias.stride(0))
     if residual is None:
         rc = lib.forgeml_hip_gemm(
@@ -198,24 +223,44 @@ def workspace_for(m: int, n: int, k: int, dtype: torch.dtype, cid: int, device: 
 KIND_NAMES = ("tiled", "few-row")
 
 
-def plan(a: torch.Tensor, b: torch.Tensor, config: KernelConfig = DEFAULT_CONFIG) -> dict:
-    """What ``matmul(a, b, config=config)`` runs: config, K slices, workspace bytes, kernel kind."""
-    cid = _check_config(config, a.dtype)
+# forgeml_hip_gemm_plan results by operand geometry: what a plan depends on
+# (shapes, element strides, dtype, config and the operands' 16-byte
+# alignment), so repeated calls, such as a compiled model's, skip the C call.
+_PLAN_CACHE: dict[tuple, tuple[int, int, int, int]] = {}
+_PLAN_CACHE_MAX = 4096
+
+
+def _plan_ids(a: torch.Tensor, b: torch.Tensor, cid: int) -> tuple[int, int, int, int]:
+    """(config id, K slices, workspace bytes, kernel kind) of a GEMM, refused as GraphError."""
     m, k = a.shape
     n = b.shape[1]
-    out = (ctypes.c_int64 * 4)()
-    rc = _native.load().forgeml_hip_gemm_plan(
-        a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1),
-        m, n, k, _DTYPE_CODES[a.dtype], cid, out,
-    )
-    if rc != _native.OK:
-        raise GraphError(f"forgeml_hip_gemm_plan failed ({rc}): {_native.last_error()}")
+    a_ptr, b_ptr = a.data_ptr(), b.data_ptr()
+    sa, sb = a.stride(), b.stride()
+    key = (m, n, k, sa, sb, a_ptr & 15, b_ptr & 15, a.dtype, cid)
+    ids = _PLAN_CACHE.get(key)
+    if ids is None:
+        out = (ctypes.c_int64 * 4)()
+        rc = _native.load().forgeml_hip_gemm_plan(
+            a_ptr, sa[0], sa[1], b_ptr, sb[0], sb[1], m, n, k, _DTYPE_CODES[a.dtype], cid, out,
+        )
+        if rc != _native.OK:
+            raise GraphError(f"forgeml_hip_gemm_plan failed ({rc}): {_native.last_error()}")
+        ids = (int(out[0]), int(out[1]), int(out[2]), int(out[3]))
+        if len(_PLAN_CACHE) >= _PLAN_CACHE_MAX:
+            _PLAN_CACHE.clear()
+        _PLAN_CACHE[key] = ids
+    return ids
+
+
+def plan(a: torch.Tensor, b: torch.Tensor, config: KernelConfig = DEFAULT_CONFIG) -> dict:
+    """What ``matmul(a, b, config=config)`` runs: config, K slices, workspace bytes, kernel kind."""
+    cid, splits, ws_bytes, kind = _plan_ids(a, b, _check_config(config, a.dtype))
     return {
-        "config": CANDIDATES[out[0]],
-        "config_id": int(out[0]),
-        "k_splits": int(out[1]),
-        "workspace_bytes": int(out[2]),
-        "kernel": KIND_NAMES[out[3]],
+        "config": CANDIDATES[cid],
+        "config_id": cid,
+        "k_splits": splits,
+        "workspace_bytes": ws_bytes,
+        "kernel": KIND_NAMES[kind],
     }
 
 
@@ -246,13 +291,15 @@ def matmul(
     what the split needs.  Launches on ``torch.cuda.current_stream()`` of
     ``a``'s device and returns ``out`` (allocated when None).
     """
-    if not torch.cuda.is_available():
+    if not _cuda_ready():
         raise GraphError("hip matmul requires a ROCm GPU visible to torch (torch.cuda)")
     _native.load()
     if not isinstance(a, torch.Tensor) or not isinstance(b, torch.Tensor):
         raise GraphError("matmul inputs must be tensors")
-    if not a.is_cuda or not b.is_cuda or a.device != b.device:
+    # Devices compared by index (get_device() builds no torch.device object).
+    if not a.is_cuda or not b.is_cuda or a.get_device() != b.get_device():
         raise GraphError("matmul inputs must be GPU tensors on the same device")
+    dev = a.get_device()
     if a.dtype not in _DTYPES or a.dtype != b.dtype:
         raise GraphError(f"matmul dtype {a.dtype} not supported or mismatched")
     if a.dim() != 2 or b.dim() != 2:
@@ -270,7 +317,7 @@ def matmul(
     if bias is not None and (
         not isinstance(bias, torch.Tensor)
         or not bias.is_cuda
-        or bias.device != a.device
+        or bias.get_device() != dev
         or bias.dtype != a.dtype
         or bias.dim() != 1
         or bias.shape[0] != n
@@ -278,14 +325,15 @@ def matmul(
         raise GraphError("bias must be a 1-D GPU tensor of output width matching dtype/device")
     if residual is not None and (
         not isinstance(residual, torch.Tensor)
-        or residual.device != a.device
+        or not residual.is_cuda
+        or residual.get_device() != dev
         or residual.dtype != a.dtype
         or tuple(residual.shape) != (m, n)
     ):
         raise GraphError("residual must be a GPU tensor of shape (M, N) matching dtype/device")
     cid = _check_config(config, a.dtype)
-    if _device_arch(a.device) != TARGET_ARCH:
-        raise GraphError(f"the HIP kernels are built for {TARGET_ARCH}; device {a.device} is {_device_arch(a.device)}")
+    if _arch_of_index(dev) != TARGET_ARCH:
+        raise GraphError(f"the HIP kernels are built for {TARGET_ARCH}; device {a.device} is {_arch_of_index(dev)}")
     if out is None:
         out = torch.empty((m, n), dtype=a.dtype, device=a.device)
     else:
@@ -293,7 +341,8 @@ def matmul(
             not isinstance(out, torch.Tensor)
             or tuple(out.shape) != (m, n)
             or out.dtype != a.dtype
-            or out.device != a.device
+            or not out.is_cuda
+            or out.get_device() != dev
             or not out.is_contiguous()
         ):
             raise GraphError("out must be a contiguous tensor of shape (M, N) matching dtype/device")
@@ -308,17 +357,22 @@ def matmul(
         ):
             raise GraphError("residual must be out itself or not share its storage")
     if workspace is not None and (
-        not isinstance(workspace, torch.Tensor) or workspace.device != a.device or workspace.dtype != torch.uint8
-        or not workspace.is_contiguous()
+        not isinstance(workspace, torch.Tensor) or not workspace.is_cuda or workspace.get_device() != dev
+        or workspace.dtype != torch.uint8 or not workspace.is_contiguous()
     ):
         raise GraphError("workspace must be a contiguous uint8 GPU tensor on the inputs' device")
-    with torch.cuda.device(a.device):
-        ws = workspace
-        if ws is None:
-            nbytes = plan(a, b, config)["workspace_bytes"]
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
-        return launch(a, b, bias, out, act=_act_code(activation, approximate), config_id=cid, workspace=ws,
-                      residual=residual)
+    ws = workspace
+    if ws is None:
+        nbytes = _plan_ids(a, b, cid)[2]
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    act = _act_code(activation, approximate)
+    # The library's per-device set-up (the LDS limit of large tiles) applies
+    # to the calling thread's current HIP device: make it the operands'
+    # device for the call when it is another one.
+    if dev == torch.cuda.current_device():
+        return launch(a, b, bias, out, act=act, config_id=cid, workspace=ws, residual=residual)
+    with torch.cuda.device(dev):
+        return launch(a, b, bias, out, act=act, config_id=cid, workspace=ws, residual=residual)
 
 
 # -- the transformer block's other hot ops ----------------------------------------
@@ -360,7 +414,7 @@ def layer_norm(x: torch.Tensor, normalized_shape, weight: torch.Tensor | None = 
     rows = xc.numel() // cols
     rc = _native.load().forgeml_hip_layer_norm(
         xc.data_ptr(), cols, None if w is None else w.data_ptr(), None if b is None else b.data_ptr(), y.data_ptr(),
-        rows, cols, float(eps), _DTYPE_CODES[x.dtype], ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream),
+        rows, cols, float(eps), _DTYPE_CODES[x.dtype], ctypes.c_void_p(_stream_handle(x.get_device())),
     )
     if rc != _native.OK:
         raise RuntimeError(f"forgeml_hip_layer_norm failed ({rc}): {_native.last_error()}")
@@ -398,7 +452,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, is_causal: b
     rc = _native.load().forgeml_hip_attention(
         qkv[0].data_ptr(), strides[0], qkv[1].data_ptr(), strides[1], qkv[2].data_ptr(), strides[2],
         out.data_ptr(), strides[3], bsz, heads, lq, lk, dim, int(bool(is_causal)), sc, _native.DTYPE_F32,
-        ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream),
+        ctypes.c_void_p(_stream_handle(q.get_device())),
     )
     if rc != _native.OK:
         raise RuntimeError(f"forgeml_hip_attention failed ({rc}): {_native.last_error()}")
