@@ -82,12 +82,6 @@ def ulp_index(x: torch.Tensor) -> torch.Tensor:
     return torch.where(bits >= 0x8000, -mag, mag)
 
 
-def from_ulp_index(o: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    bits = torch.where(o < 0, (-o) | 0x8000, o)
-    bits = torch.where(bits >= 0x8000, bits - 0x10000, bits)
-    return bits.to(torch.int16).view(dtype)
-
-
 def gelu_f64(x: torch.Tensor, approximate: str = "none") -> torch.Tensor:
     """GELU in fp64 without cancellation for negative x: x/2 erfc(-x/sqrt 2)
     (erf form) and x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3) (tanh form,
