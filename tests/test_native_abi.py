@@ -190,6 +190,36 @@ def test_gemm_plan_reports_what_runs():
     assert lib.forgeml_hip_gemm_plan(dummy, 4, 1, dummy, 1, 4, 4, 4, 4, f32, -1, None) == _native.EINVAL
 
 
+def test_cached_plans_match_the_library():
+    """kernels.plan answers from a cache keyed by operand geometry: every answer equals a
+    fresh forgeml_hip_gemm_plan call, including operands that differ only in alignment
+    (16-byte, 4-byte and 2-byte bases of the same shape plan different loaders)."""
+    lib = _native.load()
+    out = (ctypes.c_int64 * 4)()
+    kernels._PLAN_CACHE.clear()
+    for dtype, k in ((torch.float32, 1024), (torch.float32, 1531), (torch.bfloat16, 1536), (torch.bfloat16, 1531)):
+        base = torch.zeros(64 * 1536 + 16, dtype=dtype)
+        for off in (0, 1, 2, 4):
+            a = base[off:off + 33 * k].view(33, k)
+            w = torch.zeros(3000, k, dtype=dtype)
+            for b in (w.t(), w.t().contiguous()):
+                for config in (kernels.DEFAULT_CONFIG, *kernels.candidates(dtype)):
+                    try:
+                        got = kernels.plan(a, b, config)
+                    except GraphError:
+                        got = None
+                    rc = lib.forgeml_hip_gemm_plan(a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0),
+                                                   b.stride(1), 33, 3000, k, kernels._DTYPE_CODES[dtype],
+                                                   kernels.config_id(config, dtype), out)
+                    if rc != _native.OK:
+                        assert got is None, (dtype, k, off, config)
+                        continue
+                    assert got is not None and (got["config_id"], got["k_splits"], got["workspace_bytes"]) == \
+                        (out[0], out[1], out[2]), (dtype, k, off, config)
+                    assert kernels.plan(a, b, config) == got  # the cached answer is stable
+    assert kernels._PLAN_CACHE
+
+
 def test_block_kernel_argument_errors():
     lib = _native.load()
     dummy = ctypes.c_void_p(256)
