@@ -209,28 +209,27 @@ static double tile_cost(const TileConfig& t, int64_t m, int64_t n, int64_t k, in
 }
 
 // Shape heuristic behind FORGEML_CONFIG_AUTO for the tiled kernels: the
-// lowest tile_cost, larger tiles winning within 1 %.  The 8-wave 16-bit tile
-// is offered only when both operands are K-contiguous (its register budget
-// does not fit the transposing loaders); layouts whose kernels exist only
-// for small tiles choose among those, and 16-bit element loads (whose staged
-// values and addresses outgrow the registers of larger tiles) use 64x64.
-// Tiles whose grid would reach 2^32 work-items are skipped; -1 when no
-// allowed tile fits.
+// lowest tile_cost, larger tiles winning within 1 %.  Only tiles built for
+// the operand combination the layout runs on them are offered
+// (combo_supported, the launch's own test): the 8-wave 16-bit tile takes
+// K-contiguous operands only (its register budget does not fit the
+// transposing loaders), and 16-bit element loads, including a pair of modes
+// that steps down to them, run on 64x64 (their staged values and addresses
+// outgrow the registers of larger tiles).  Layouts whose kernels exist only
+// for small tiles choose among those.  Tiles whose grid would reach 2^32
+// work-items are skipped; -1 when no allowed tile fits.
 static int select_config(int64_t m, int64_t n, int64_t k, int dtype, int ma, int mb) {
   const int dclass = dclass_of(dtype);
   const int esz = esize_of(dtype);
-  const bool all_k = ma == MODE_K && mb == MODE_K;
-  const int64_t max_area = (dclass == 1 && (ma == MODE_G || mb == MODE_G)) ? 64 * 64
-                           : needs_small_tile(ma, mb)                     ? kSmallTileArea
-                                                                          : INT64_MAX;
+  const int64_t max_area = needs_small_tile(ma, mb) ? kSmallTileArea : INT64_MAX;
   int best = -1;
   double best_cost = 0.0;
   for (int id = 0; id < kNumTiles; ++id) {
     const TileConfig& t = kTiles[id];
     if (t.dclass != dclass || t.kind != KIND_TILED) continue;
-    if (t.wm * t.wn > 4 && dclass == 1 && !all_k) continue;
     const int64_t area = (int64_t)t.bm * t.bn;
     if (area > max_area) continue;
+    if (!combo_supported(t.dclass, t.bm, t.bn, t.wm * t.wn, combo_of(ma, mb, area <= kSmallTileArea))) continue;
     if (launch_items(t, m, n, split_plan(t, m, n, k, esz).splits) >= kMaxItems) continue;
     const double cost = tile_cost(t, m, n, k, esz);
     bool take = best < 0 || cost < best_cost * 0.99;  // clearly cheaper

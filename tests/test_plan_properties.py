@@ -113,3 +113,29 @@ def test_select_config_matches_the_plan_for_aligned_k_contiguous_operands(lib, m
     rc, (planned, _, _, _) = _plan(lib, (m, n, k, dtype, esz, ld, 1, 1, ld, 4096, 1 << 20))
     assert rc == _native.OK and planned == cid
     assert cid == lib.forgeml_hip_select_config(m, n, k, dtype)  # deterministic
+
+
+def test_auto_plans_a_built_tile_for_every_layout(lib):
+    """FORGEML_CONFIG_AUTO plans a config the launch accepts for every operand layout pair,
+    every residue of M and K mod 8, row padding and base offset: the shape heuristic offers
+    only tiles built for the operand combination the layout runs on them (a transposed A
+    with 4-byte B rows steps down to element loads, which 16-bit tiles above 64x64 lack)."""
+    failures = []
+    for dtype, esz in DTYPES:
+        for m, n in ((1584, 109), (1585, 1000), (1736, 2134), (2808, 1919)):
+            for k in (1228, 1662, 4096, 4100, 4101):
+                for pad in (0, 1, 2):
+                    for a_layout in ("row", "col", "strided"):
+                        for b_layout in ("wt", "kn", "strided"):
+                            for a_off in (0, 1):
+                                sam, sak = {"row": (k + pad, 1), "col": (1, m + pad), "strided": (2 * (k + pad), 2)}[a_layout]
+                                sbk, sbn = {"wt": (1, k + pad), "kn": (n + pad, 1), "strided": (2, 2 * (k + pad))}[b_layout]
+                                p = (m, n, k, dtype, esz, sam, sak, sbk, sbn, 4096 + esz * a_off, 1 << 20)
+                                rc, (cid, _, _, _) = _plan(lib, p)
+                                if rc != _native.OK:
+                                    failures.append((p, _native.last_error()))
+                                    continue
+                                rc2, _ = _plan(lib, p, cid)  # the chosen config is accepted as such
+                                if rc2 != _native.OK:
+                                    failures.append((p, cid, _native.last_error()))
+    assert not failures, failures[:5]
