@@ -279,7 +279,7 @@ int forgeml_hip_config_info(int32_t id, int32_t* out) {
   const int stages = (int64_t)t.bm * t.bn <= 64 * 64 ? 4 : 2;
   out[5] = stages;
   out[6] = (int32_t)kMaxSplit;
-  out[7] = stages * (t.bm + t.bn) * kRowBytes;
+  out[7] = stages * (t.bm + t.bn) * kRowBytes + (t.dclass != 0 && t.bm * t.bn >= 256 * 256 && t.wm * t.wn == 8 ? kLutBytes : 0);
   return FORGEML_OK;
 }
 

@@ -28,7 +28,8 @@
 //    blocks of v_mfma_f32_16x16x32_{bf16,f16}, whose LDS rows use a swizzle
 //    that repeats every 16 rows.
 //  * The epilogue rounds to the output dtype, adds the bias in fp32, rounds
-//    again, applies GELU (erf or tanh) or clamp_min(x,0) in registers and
+//    again, applies GELU (erf or tanh; for bf16 on the 8-wave 256x256 tile
+//    from a table of its values in LDS) or clamp_min(x,0) in registers and
 //    stores once.
 //  * Workgroup ids are remapped so each XCD (8 per MI355X, each with its own
 //    L2) works on a contiguous, M-grouped block of output tiles.
@@ -65,7 +66,8 @@ struct GemmArgs {
   int act;
   int has_bias;
   // Optional residual R[M,N] (element (m,n) at res + m*srm + n*srn elements),
-  // added after the activation: C = rnd(act(...) + R).  res may equal c.
+  // added to the rounded activation: C = rnd(rnd(act(...)) + R), as an add
+  // kernel reading the GEMM's output would compute.  res may equal c.
   const char* res;
   int64_t srm, srn;
   int tiles_m, tiles_n;
@@ -202,6 +204,47 @@ __device__ __forceinline__ float activate(float v) {
   else if constexpr (ACT == ACT_GELU_TANH) return DT == DT_F32 ? gelu_tanh(v) : gelu_tanh_16(v);
   else if constexpr (ACT == ACT_RELU) return v < 0.0f ? 0.0f : v;  // clamp_min keeps NaN
   else return v;
+}
+
+// GELU of bf16 values by table.  The activation's input is itself a bf16
+// value (the bias sum is rounded first), so a tile with many outputs per
+// workgroup (the 8-wave 256x256 tile: 65536; the 4-wave one has no
+// registers to spare beside its accumulators) evaluates the activation once per
+// bf16 input of magnitude in [2^-16, 16), either sign (20 binades of 128
+// mantissas), into LDS, rounded to bf16 as the store would round it, and
+// its epilogue looks the outputs up: the same bits as evaluating each one,
+// for about a quarter of the vector ALU work.  Inputs outside the table
+// (magnitudes below 2^-16 or from 16 up, zeros, infinities, NaN) take the
+// arithmetic path.  Entry i: sign i / kLutSpan, bf16 exponent and mantissa
+// bits (kLutLoExp << 7) + i % kLutSpan.
+constexpr int kLutLoExp = 127 - 16;
+constexpr int kLutSpan = 20 * 128;
+constexpr int kLutBytes = 2 * kLutSpan * 2;
+
+template <int DT, int BM, int BN, int WAVES>
+constexpr bool gelu_lut_tile() {
+  return DT == DT_BF16 && BM * BN >= 256 * 256 && WAVES == 8;
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) {
+  return __builtin_bit_cast(uint16_t, (__bf16)v);
+}
+
+template <int ACT>
+__device__ __forceinline__ void build_gelu_lut(uint16_t* lut, int tid, int nt) {
+  for (int i = tid; i < 2 * kLutSpan; i += nt) {
+    const int neg = i >= kLutSpan;
+    const uint32_t bits = ((uint32_t)neg << 15) | (((uint32_t)kLutLoExp << 7) + (uint32_t)(i - neg * kLutSpan));
+    lut[i] = bf16_bits(activate<DT_BF16, ACT>(bf16_to_f32(bits)));
+  }
+}
+
+// Table index of bf16 value x (held in a float), and whether it is inside.
+__device__ __forceinline__ bool gelu_lut_index(float x, uint32_t& idx) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t t = ((u >> 16) & 0x7fffu) - ((uint32_t)kLutLoExp << 7);
+  idx = t + (u >> 31) * (uint32_t)kLutSpan;
+  return t < (uint32_t)kLutSpan;
 }
 
 // ---------------------------------------------------------------------------
@@ -739,9 +782,10 @@ __device__ __forceinline__ void write_band(const f32x4 (&acc)[TM2][TN2], int tm,
 
 // STREAM: non-temporal output stores (the final C); split-K partial planes,
 // which the reduce kernel reads right after, are stored plainly.
-template <int DT, int ACT, int TM, int TN, bool INTERIOR, bool STREAM, class Acc>
+// LUT: the activation by table (gelu_lut_tile), from `lut` in LDS.
+template <int DT, int ACT, int TM, int TN, bool INTERIOR, bool STREAM, bool LUT, class Acc>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, float* buf, int row_base, int col_base,
-                                         int lane) {
+                                         int lane, const uint16_t* lut) {
   constexpr int ESZ = DTraits<DT>::ESZ;
   constexpr int EPV = 16 / ESZ;      // outputs per lane per row segment
   constexpr int CPR = 32 / EPV;      // lanes per 32-column block row
@@ -776,14 +820,35 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
           v[j + 2] = f.z;
           v[j + 3] = f.w;
         }
+        if constexpr (LUT) {
+          // One table read per output when all of the lane's segment is
+          // inside the table, else the arithmetic form for the segment.
+          float x[EPV];
+          uint32_t idx[EPV];
+          bool inside = true;
 #pragma unroll
-        for (int j = 0; j < EPV; ++j) {
-          float x = round_to<DT>(v[j]);
-          if (p.has_bias) x = round_to<DT>(x + bias[tn][j]);
-          v[j] = activate<DT, ACT>(x);
+          for (int j = 0; j < EPV; ++j) {
+            x[j] = round_to<DT>(v[j]);
+            if (p.has_bias) x[j] = round_to<DT>(x[j] + bias[tn][j]);
+            inside &= gelu_lut_index(x[j], idx[j]);
+          }
+          if (inside) {
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) v[j] = bf16_to_f32(lut[idx[j]]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) v[j] = round_to<DT>(activate<DT, ACT>(x[j]));
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < EPV; ++j) {
+            float x = round_to<DT>(v[j]);
+            if (p.has_bias) x = round_to<DT>(x + bias[tn][j]);
+            v[j] = activate<DT, ACT>(x);
+          }
         }
         if (p.res != nullptr && (INTERIOR || row < p.m)) {
-          // Residual add after the activation, rounded like torch's add.
+          // Residual add to the rounded activation, rounded like torch's add.
           const char* rp = p.res + ((int64_t)row * p.srm + (int64_t)col * p.srn) * ESZ;
           if (p.srn == 1 && (((uintptr_t)rp) & 15) == 0 && (INTERIOR || col + EPV <= p.n)) {
             const u32x4 w = *(const u32x4*)rp;
@@ -793,12 +858,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
               const float r = ESZ == 4 ? __uint_as_float(word)
                                        : (DT == DT_BF16 ? bf16_to_f32((word >> (16 * (j & 1))) & 0xffffu)
                                                         : f16_to_f32((word >> (16 * (j & 1))) & 0xffffu));
-              v[j] = round_to<DT>(v[j] + r);
+              v[j] = round_to<DT>(round_to<DT>(v[j]) + r);
             }
           } else {
 #pragma unroll
             for (int j = 0; j < EPV; ++j)
-              if (INTERIOR || col + j < p.n) v[j] = round_to<DT>(v[j] + residual_at<DT>(p, row, col + j));
+              if (INTERIOR || col + j < p.n) v[j] = round_to<DT>(round_to<DT>(v[j]) + residual_at<DT>(p, row, col + j));
           }
         }
         if (INTERIOR || row < p.m) {
@@ -830,11 +895,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
   }
 }
 
-template <int DT, int ACT, int TM, int TN, bool STREAM = true, class Acc>
+template <int DT, int ACT, int TM, int TN, bool STREAM = true, bool LUT = false, class Acc>
 __device__ __forceinline__ void epilogue_dispatch(const GemmArgs& p, const Acc& acc, float* buf, int row_base,
-                                                  int col_base, int lane, bool interior) {
-  if (interior) epilogue<DT, ACT, TM, TN, true, STREAM>(p, acc, buf, row_base, col_base, lane);
-  else epilogue<DT, ACT, TM, TN, false, STREAM>(p, acc, buf, row_base, col_base, lane);
+                                                  int col_base, int lane, bool interior,
+                                                  const uint16_t* lut = nullptr) {
+  if (interior) epilogue<DT, ACT, TM, TN, true, STREAM, LUT>(p, acc, buf, row_base, col_base, lane, lut);
+  else epilogue<DT, ACT, TM, TN, false, STREAM, LUT>(p, acc, buf, row_base, col_base, lane, lut);
 }
 
 // ---------------------------------------------------------------------------
@@ -948,6 +1014,14 @@ void fused_gemm_kernel(GemmArgs p) {
   lb.issue(kt0, smem + BM * kRowBytes);
   la.commit(smem);
   lb.commit(smem + BM * kRowBytes);
+  // The GELU table, past the ring, while the first stage lands (the barrier
+  // before the main loop orders it before the epilogue's reads).
+  constexpr bool LUT_TILE = gelu_lut_tile<DT, BM, BN, WM * WN>();
+  uint16_t* const lut = (uint16_t*)(smem + S * STAGE);
+  if constexpr (LUT_TILE) {
+    if (p.splits == 1 && p.act == ACT_GELU_ERF) build_gelu_lut<ACT_GELU_ERF>(lut, threadIdx.x, NT);
+    else if (p.splits == 1 && p.act == ACT_GELU_TANH) build_gelu_lut<ACT_GELU_TANH>(lut, threadIdx.x, NT);
+  }
   if constexpr (SPLIT_DMA) {
     la.template issue_part<0, HA>(kt0 + 1, smem + STAGE);
     lb.template issue_part<0, HB>(kt0 + 1, smem + STAGE + BM * kRowBytes);
@@ -1030,8 +1104,12 @@ void fused_gemm_kernel(GemmArgs p) {
   const bool interior = row0 + BM <= p.m && col0 + BN <= p.n && (p.n % DTraits<DT>::VEC) == 0 &&
                         (((uintptr_t)p.c) & 15) == 0;
   switch (p.act) {
-    case ACT_GELU_ERF: epilogue_dispatch<DT, ACT_GELU_ERF, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
-    case ACT_GELU_TANH: epilogue_dispatch<DT, ACT_GELU_TANH, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
+    case ACT_GELU_ERF:
+      epilogue_dispatch<DT, ACT_GELU_ERF, TM, TN, true, LUT_TILE>(p, acc, buf, row_base, col_base, lane, interior, lut);
+      break;
+    case ACT_GELU_TANH:
+      epilogue_dispatch<DT, ACT_GELU_TANH, TM, TN, true, LUT_TILE>(p, acc, buf, row_base, col_base, lane, interior, lut);
+      break;
     case ACT_RELU: epilogue_dispatch<DT, ACT_RELU, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
     default: epilogue_dispatch<DT, ACT_NONE, TM, TN>(p, acc, buf, row_base, col_base, lane, interior); break;
   }
@@ -1047,7 +1125,7 @@ struct ReduceArgs {
   const float* ws;
   const char* bias;
   char* c;
-  const char* res;  // optional residual, added after the activation
+  const char* res;  // optional residual, added to the rounded activation
   int64_t srm, srn;
   int64_t sbi;
   int64_t mn;  // M * N
@@ -1089,7 +1167,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs p) {
     float x = round_to<DT>(v[j]);
     if (p.has_bias && j < cnt) x = round_to<DT>(x + load_as_f32<DT>(p.bias + (int64_t)col * p.sbi * ESZ));
     x = activate<DT, ACT>(x);
-    if (p.res != nullptr && j < cnt) x = round_to<DT>(x + load_as_f32<DT>(p.res + (row * p.srm + (int64_t)col * p.srn) * ESZ));
+    if (p.res != nullptr && j < cnt)
+      x = round_to<DT>(round_to<DT>(x) + load_as_f32<DT>(p.res + (row * p.srm + (int64_t)col * p.srn) * ESZ));
     v[j] = x;
     if (col + 1 == p.n) {
       col = 0;

@@ -74,7 +74,7 @@ int launch_reduce(const GemmArgs& p, hipStream_t stream) {
 template <int DT, int BM, int BN, int WM, int WN, int AMODE, int BMODE, int S>
 int launch_ring(const GemmArgs& p, hipStream_t stream) {
   constexpr int NT = WM * WN * 64;
-  constexpr int LDS = S * (BM + BN) * kRowBytes;
+  constexpr int LDS = S * (BM + BN) * kRowBytes + (gelu_lut_tile<DT, BM, BN, WM * WN>() ? kLutBytes : 0);
   const void* fn = reinterpret_cast<const void*>(&fused_gemm_kernel<DT, BM, BN, WM, WN, AMODE, BMODE, S>);
   if constexpr (LDS > 65536) {
     // Above 64 KiB the dynamic LDS limit must be raised once per device

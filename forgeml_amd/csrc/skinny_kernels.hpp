@@ -178,7 +178,7 @@ __device__ __forceinline__ void skinny_store(const GemmArgs& p, float v, int row
   float x = round_to<DT>(v);
   if (p.has_bias) x = round_to<DT>(x + load_as_f32<DT>(p.bias + (int64_t)col * p.sbi * ESZ));
   x = activate<DT, ACT>(x);
-  if (p.res != nullptr) x = round_to<DT>(x + residual_at<DT>(p, row, col));
+  if (p.res != nullptr) x = round_to<DT>(round_to<DT>(x) + residual_at<DT>(p, row, col));
   store_from_f32<DT>(p.c + ((int64_t)row * p.n + col) * ESZ, x);
 }
 

@@ -281,7 +281,7 @@ def matmul(
     ``activation`` is "none", "gelu" (``approximate`` "none" = erf, "tanh")
     or "relu" (clamp_min(x, 0), the executor's relu slot writer fused into
     the epilogue).  ``residual`` (keyword only, not in the reference's
-    signature) adds an [M, N] tensor after the activation in the same
+    signature) adds an [M, N] tensor to the rounded activation in the same
     epilogue, as the reference's following ``add`` node would; it may be
     ``out`` itself.  ``workspace`` (keyword only, not in the reference's
     signature): a uint8 GPU buffer for split-K partial sums, at least

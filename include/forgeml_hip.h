@@ -61,7 +61,8 @@ extern "C" {
  * [4] waves per workgroup     [5] LDS stages (at most: a launch may ring
  *     through fewer, as the grid size and operand layout decide)
  * [6] split_k (1 = none; >1 = K split over workgroups, needs a workspace)
- * [7] LDS bytes per workgroup (at the most stages) */
+ * [7] LDS bytes per workgroup (at the most stages; for the 8-wave 16-bit
+ *     256x256 tile including the 10 KiB table of bf16 GELU values) */
 
 /*
  * Fused GEMM + bias + activation.  Replaces `launch` in
@@ -96,7 +97,7 @@ int forgeml_hip_gemm(const void* a, int64_t sam, int64_t sak,
 /*
  * Fused GEMM + bias + activation + residual add:
  *
- *     C = rnd( act( rnd( rnd(A·B) + bias ) ) + R )
+ *     C = rnd( rnd( act( rnd( rnd(A·B) + bias ) ) ) + R )
  *
  * i.e. forgeml_hip_gemm followed, in the same epilogue, by the `add` node
  * the reference's executor runs next on the GEMM's result (the residual

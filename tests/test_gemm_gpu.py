@@ -560,6 +560,36 @@ def test_eight_wave_tile(gpu, dtype, m, n, k):
     assert torch.equal(kernels.matmul(a_d, b_d, bias_d, config=cfg), kernels.matmul(a_d, b_d, bias_d, config=cfg))
 
 
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_bf16_gelu_table_equals_arithmetic_form(gpu, approximate):
+    """The 8-wave tile's GELU table against the per-element form of the 64x64
+    tile, on every bf16 bit pattern as a pre-activation (C = A[:, 0], exact:
+    K = 8 and B one-hot), alone, after a bias per column and before a
+    residual: the same bits everywhere (NaN where NaN)."""
+    dtype = torch.bfloat16
+    m, n, k = 65536, 256, 8
+    a = torch.zeros(m, k, dtype=dtype)
+    a[:, 0] = torch.arange(m, dtype=torch.int32).to(torch.int16).view(dtype)
+    w = torch.zeros(n, k, dtype=dtype)
+    w[:, 0] = 1.0
+    g = torch.Generator().manual_seed(case_seed("gelu_table", approximate))
+    bias = (torch.randn(n, generator=g) * 4).to(dtype)
+    r = torch.randn(m, n, generator=g).to(dtype)
+    a_d, b_d = a.to(gpu), w.to(gpu).t()
+    (arith,) = [c for c in kernels.candidates(dtype) if (c.block_m, c.block_n) == (64, 64)]
+    table = _eight_wave_config(dtype)
+    for bias_d, res_d in ((None, None), (bias.to(gpu), None), (bias.to(gpu), r.to(gpu))):
+        what = f"GELU table {approximate} bias={bias_d is not None} residual={res_d is not None}"
+        _say(what)
+        outs = [kernels.matmul(a_d, b_d, bias_d, activation="gelu", approximate=approximate, residual=res_d,
+                               config=cfg).cpu() for cfg in (table, arith)]
+        got, want = (o.view(torch.int16) for o in outs)
+        nan = outs[1].isnan()
+        assert torch.equal(outs[0].isnan(), nan), what
+        diff = (got != want) & ~nan
+        assert not diff.any(), f"{what}: {int(diff.sum())} outputs differ, first at {diff.nonzero()[0].tolist()}"
+
+
 # -- seeded random problems through the few-row kernel ----------------------------
 
 def test_few_row_kernel_random_problems(gpu):
