@@ -834,11 +834,19 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
             for (int j = 0; j < EPV; ++j) v[j] = round_to<DT>(activate<DT, ACT>(x[j]));
           }
         } else {
+          // Activations that commute with rounding (none, relu) skip the
+          // rounding of their input: the store rounds, and so does the
+          // residual add's first step.
+          constexpr bool KEEP = ACT == ACT_NONE || ACT == ACT_RELU;
+          if (p.has_bias) {
 #pragma unroll
-          for (int j = 0; j < EPV; ++j) {
-            float x = round_to<DT>(v[j]);
-            if (p.has_bias) x = round_to<DT>(x + bias[tn][j]);
-            v[j] = activate<DT, ACT>(x);
+            for (int j = 0; j < EPV; ++j) {
+              const float x = round_to<DT>(v[j]) + bias[tn][j];
+              v[j] = activate<DT, ACT>(KEEP ? x : round_to<DT>(x));
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < EPV; ++j) v[j] = activate<DT, ACT>(KEEP ? v[j] : round_to<DT>(v[j]));
           }
         }
         if (p.res != nullptr && (INTERIOR || row < p.m)) {
