@@ -835,18 +835,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const Acc& acc, floa
           }
         } else {
           // Activations that commute with rounding (none, relu) skip the
-          // rounding of their input: the store rounds, and so does the
+          // rounding of the bias sum: the store rounds, and so does the
           // residual add's first step.
           constexpr bool KEEP = ACT == ACT_NONE || ACT == ACT_RELU;
-          if (p.has_bias) {
 #pragma unroll
-            for (int j = 0; j < EPV; ++j) {
-              const float x = round_to<DT>(v[j]) + bias[tn][j];
-              v[j] = activate<DT, ACT>(KEEP ? x : round_to<DT>(x));
-            }
-          } else {
-#pragma unroll
-            for (int j = 0; j < EPV; ++j) v[j] = activate<DT, ACT>(KEEP ? v[j] : round_to<DT>(v[j]));
+          for (int j = 0; j < EPV; ++j) {
+            float x = round_to<DT>(v[j]);
+            if (p.has_bias) x = KEEP ? x + bias[tn][j] : round_to<DT>(x + bias[tn][j]);
+            v[j] = activate<DT, ACT>(x);
           }
         }
         if (p.res != nullptr && (INTERIOR || row < p.m)) {

@@ -319,3 +319,59 @@ def test_tiles_refuse_layouts_they_are_not_built_for():
         assert plan(1024, 1, 1024, cid) == _native.OK
     # AUTO picks a built tile for the odd-K layout.
     assert plan(1531, 1, 1531, -1) == _native.OK and kernels.CANDIDATES[out[0]].block_m == 64
+
+
+def _gfx950_kernel_metadata(path):
+    """The amdhsa.kernels metadata of every gfx950 code object the library
+    embeds: clang offload bundles (one per translation unit) hold ELF code
+    objects whose AMDGPU note (type 32) is a msgpack map."""
+    import struct
+
+    msgpack = pytest.importorskip("msgpack")
+    data = path.read_bytes()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    kernels_md = []
+    start = data.find(magic)
+    while start >= 0:
+        (count,) = struct.unpack_from("<Q", data, start + len(magic))
+        pos = start + len(magic) + 8
+        for _ in range(count):
+            off, size, tlen = struct.unpack_from("<QQQ", data, pos)
+            triple = data[pos + 24:pos + 24 + tlen].decode()
+            pos += 24 + tlen
+            if not triple.endswith("gfx950") or size == 0:
+                continue
+            elf = data[start + off:start + off + size]
+            assert elf[:4] == b"\x7fELF", triple
+            shoff, = struct.unpack_from("<Q", elf, 0x28)
+            shentsize, shnum = struct.unpack_from("<HH", elf, 0x3A)
+            for s in range(shnum):
+                sh = shoff + s * shentsize
+                if struct.unpack_from("<I", elf, sh + 4)[0] != 7:  # SHT_NOTE
+                    continue
+                noff, nsize = struct.unpack_from("<QQ", elf, sh + 0x18)
+                p = noff
+                while p < noff + nsize:
+                    namesz, descsz, ntype = struct.unpack_from("<III", elf, p)
+                    name = elf[p + 12:p + 12 + namesz].rstrip(b"\0")
+                    desc = p + 12 + ((namesz + 3) & ~3)
+                    if name == b"AMDGPU" and ntype == 32:
+                        kernels_md += msgpack.unpackb(elf[desc:desc + descsz], raw=False, strict_map_key=False)["amdhsa.kernels"]
+                    p = desc + ((descsz + 3) & ~3)
+        start = data.find(magic, start + 1)
+    return kernels_md
+
+
+def test_no_kernel_uses_scratch():
+    """Register spills go to per-lane scratch memory, a slow path the tiles are
+    sized to avoid (the 4-wave 256x256 tile's accumulators fill the AGPRs, and
+    two epilogue changes once pushed it to 1 KB of scratch per lane).  Read the
+    built library's own gfx950 code-object metadata and require none."""
+    if not _native.LIBRARY_PATH.exists():
+        pytest.skip("library not built")
+    md = _gfx950_kernel_metadata(_native.LIBRARY_PATH)
+    names = [k[".name"] for k in md]
+    assert any("fused_gemm_kernel" in n for n in names) and any("attention_kernel" in n for n in names)
+    spilled = [(k[".name"], k.get(".private_segment_fixed_size"), k.get(".vgpr_spill_count"))
+               for k in md if k.get(".private_segment_fixed_size", 0) or k.get(".vgpr_spill_count", 0)]
+    assert not spilled, spilled
