@@ -468,7 +468,7 @@ BLOCK_GEMMS = [("qkv_4096x2304x768", 4096, 2304, 768, "none", (64, 64, 4)),
                ("ffn_up_4096x3072x768_gelu", 4096, 3072, 768, "gelu", (128, 128, 4)),
                ("ffn_down_4096x768x3072", 4096, 768, 3072, "none", (64, 64, 4)),
                ("out_proj_4096x768x768", 4096, 768, 768, "none", (64, 64, 4)),
-               ("headline_4096x4096x4096_gelu", 4096, 4096, 4096, "gelu", (256, 128, 8))]
+               ("headline_4096x4096x4096_gelu", 4096, 4096, 4096, "gelu", (256, 256, 8))]
 
 
 def block_gemm_launches(steps: int):

@@ -458,10 +458,10 @@ static int gemm_impl(const void* a, int64_t sam, int64_t sak, const void* b, int
   // Tile rows per group of the workgroup order (tile_coords): an XCD (32 CUs)
   // runs about C = 32 * occ tiles at once, gsz rows by C / gsz columns of
   // tiles, which stream gsz * BM rows of A and C / gsz * BN columns of B
-  // through its L2 together; gsz = sqrt(C * BN / BM) minimises that.  It is 4
-  // for the 256x128 fp32 tile (fp32 4096^3: HBM fetch -20 %, same time) and 6
-  // for the 256x256 16-bit tiles (bf16 8192x14336x4096: 861 -> 824 us); 8,
-  // the earlier fixed choice, for the tiles that share a CU.
+  // through its L2 together; gsz = sqrt(C * BN / BM) minimises that.  It is 6
+  // for the 256x256 tiles (bf16 8192x14336x4096: 861 -> 824 us; a 256x128
+  // fp32 tile took 4: fp32 4096^3 HBM fetch -20 %, same time); 8, the
+  // earlier fixed choice, for the tiles that share a CU.
   const int gsz = (int)lround(sqrt(32.0 * t.occ * t.bn / t.bm));
   p.group_m = p.tiles_m < gsz ? p.tiles_m : gsz;
   p.splits = plan.split.splits;

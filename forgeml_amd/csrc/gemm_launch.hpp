@@ -30,10 +30,12 @@ constexpr int kSmallTileArea = 128 * 128;
 // (COMBO_G_*) stage 32 packed values per thread, and tiles above 64x64 then
 // run out of registers beside their accumulators and spill to scratch; the
 // 8-wave 16-bit tile's budget fits only the DMA loaders of two K-contiguous
+// operands, and the 8-wave fp32 tile's everything but element loads of both
 // operands.  Those pairs are not built, and the planner refuses a request
 // for one; the shape heuristic never chooses them.
 constexpr bool combo_supported(int dclass, int bm, int bn, int waves, int combo) {
   if (dclass == 1 && waves > 4 && combo != COMBO_K_K) return false;
+  if (dclass == 0 && waves > 4 && combo == COMBO_G_G) return false;
   if (dclass == 1 && bm * bn > 64 * 64 && (combo == COMBO_G_G || combo == COMBO_G_MN)) return false;
   return true;
 }

@@ -15,7 +15,7 @@
 #define FORGEML_F32_TILES(X)       \
   X(128, 128, 2, 2, 2, 100, 88)    \
   X(64, 64, 2, 2, 2, 90, 90)       \
-  X(256, 128, 4, 2, 1, 100, 100)
+  X(256, 256, 2, 4, 1, 100, 100)
 
 #define FORGEML_H16_TILES(X)       \
   X(256, 256, 2, 2, 1, 91, 91)     \

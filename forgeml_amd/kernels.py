@@ -54,7 +54,7 @@ DEFAULT_CONFIG = KernelConfig()
 # (block_m, block_n, waves, LDS stages); the 64x64 tiles keep up to four stages
 # in flight when both operands are K-contiguous (two on grids of more than two
 # workgroups per CU, where more resident workgroups hide latency better).
-_FP32_TILES = ((128, 128, 4, 2), (64, 64, 4, 4), (256, 128, 8, 2))
+_FP32_TILES = ((128, 128, 4, 2), (64, 64, 4, 4), (256, 256, 8, 2))
 _H16_TILES = ((256, 256, 4, 2), (128, 128, 4, 2), (64, 64, 4, 4), (256, 256, 8, 2))
 # The few-row kernels come last: up to 64 rows, 16 columns per workgroup, 8
 # waves splitting K in chunks of 16 fp32 / 32 16-bit elements, up to 4 chunks

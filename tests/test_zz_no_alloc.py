@@ -86,13 +86,13 @@ def test_noalloc_refuses_beyond_its_scratch(gpu):
     lib = _native.load()
     limit = lib.forgeml_hip_noalloc_scratch_bytes()
     assert limit == 32 << 20
-    # 2048 x 1920 outputs on the 256x128 fp32 tile are 120 tiles, so K is
-    # split 5 ways: 5 planes of 2048 x 1920 fp32 need 78.6 MB, past the array.
+    # 2048 x 1920 outputs on the 256x256 fp32 tile are 64 tiles, so K is
+    # split 8 ways: 8 planes of 2048 x 1920 fp32 need 125.8 MB, past the array.
     m, n, k = 2048, 1920, 4096
     out = (ctypes.c_int64 * 4)()
     a = torch.empty(m, k, device=gpu)
     b = torch.empty(k, n, device=gpu)  # [K, N] row-major
-    cid = kernels.config_id(kernels.candidates(torch.float32)[2], torch.float32)  # 256x128
+    cid = kernels.config_id(kernels.candidates(torch.float32)[2], torch.float32)  # 256x256
     rc = lib.forgeml_hip_gemm_plan(a.data_ptr(), k, 1, b.data_ptr(), n, 1, m, n, k, _native.DTYPE_F32, cid, out)
     assert rc == _native.OK and out[2] > limit, list(out)
     c = torch.empty(m, n, device=gpu)
