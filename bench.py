@@ -579,6 +579,9 @@ def main() -> int:
     m = n = k = 4096
     head = gemm_workload("fused_addmm_bias_gelu_erf_fp32_4096", m, n, k, torch.float32,
                          steps=args.steps, warmup=args.warmup)
+    traffic_key = (f"fp32 {m}x{n}x{k} B=W^T tile={head['tile'][0]}x{head['tile'][1]}x"
+                   f"{head['tile'][2]} waves={head['tile'][3]}")
+    traffic = _measured_traffic(traffic_key)
     result = {
         "metric": "fused linear+bias+GELU TFLOP/s (fp32 M=N=K=4096, B=W^T, erf GELU)",
         "value": round(head["tflops"], 3),
@@ -600,10 +603,10 @@ def main() -> int:
             "peak": PEAK_TFLOPS[torch.float32],
             "unit": "TFLOP/s",
             "frac": round(head["kernel_tflops"] / PEAK_TFLOPS[torch.float32], 4),
-            "traffic": _measured_traffic(f"fp32 {m}x{n}x{k} B=W^T tile={head['tile'][0]}x{head['tile'][1]}x"
-                                         f"{head['tile'][2]} waves={head['tile'][3]}"),
-            "traffic_source": "committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs of this kernel tile "
-                              "(profiles/hbm_traffic.json), not measured in this run",
+            "traffic": traffic,
+            "traffic_source": ("committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs of this kernel tile "
+                               "(profiles/hbm_traffic.json), not measured in this run") if traffic is not None
+                              else f"no committed counter run for {traffic_key}",
             "kernel_us_avg": round(head["kernel_ms_avg"] * 1e3, 2),
         },
         "gate": head["gate"],
