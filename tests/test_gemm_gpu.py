@@ -526,12 +526,13 @@ def _eight_wave_config(dtype):
     return cfg
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(392, 328, 520), (256, 256, 64), (1000, 3000, 1536), (512, 512, 8192), (300, 700, 72),
                                    (4096, 2048, 1000)])
 def test_eight_wave_tile(gpu, dtype, m, n, k):
-    """Edge tiles in M and N, K tails shorter than a stage, one-stage K, and a
-    grid small enough to split K; every epilogue, held to the contract."""
+    """The 8-wave 256x256 tiles (16-bit and fp32): edge tiles in M and N, K
+    tails shorter than a stage, one-stage K, and a grid small enough to split
+    K; every epilogue, 16-bit outputs also held to the contract."""
     cfg = _eight_wave_config(dtype)
     seed = case_seed("eight_wave", m, n, k, dtype)
     a, b, bias = gemm_inputs(m, n, k, dtype, seed=seed, b_layout="nt")
@@ -546,7 +547,8 @@ def test_eight_wave_tile(gpu, dtype, m, n, k):
             bb, bb_d = (bias, bias_d) if with_bias else (None, None)
             got = kernels.matmul(a_d, b_d, bb_d, activation=activation, approximate=approximate, config=cfg)
             _gate(got, reference_cpu(a, b, bb, activation, approximate), k, what)
-            _contract(got, a, b, bb, activation, approximate, what, acc=acc)
+            if dtype != torch.float32:
+                _contract(got, a, b, bb, activation, approximate, what, acc=acc)
     # residual after the activation, into a fresh output and in place
     g = torch.Generator().manual_seed(seed + 1)
     r = torch.randn(m, n, generator=g).to(dtype)
