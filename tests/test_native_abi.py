@@ -292,10 +292,11 @@ def test_launch_size_limits():
 
 
 def test_tiles_refuse_layouts_they_are_not_built_for():
-    """16-bit tiles above 64x64 are not built for element loads (an odd K), and
+    """16-bit tiles above 64x64 are not built for element loads (an odd K),
     the 8-wave 16-bit tile only for two K-contiguous operands with 16-byte
-    rows: an explicit request is refused with ECONFIG; AUTO plans a built
-    tile (host-side planning only: nothing is launched)."""
+    rows, and the 8-wave fp32 tile not for element loads of both operands:
+    an explicit request is refused with ECONFIG; AUTO plans a built tile
+    (host-side planning only: nothing is launched)."""
     lib = _native.load()
     out = (ctypes.c_int64 * 4)()
     dummy = ctypes.c_void_p(256)
@@ -319,6 +320,14 @@ def test_tiles_refuse_layouts_they_are_not_built_for():
         assert plan(1024, 1, 1024, cid) == _native.OK
     # AUTO picks a built tile for the odd-K layout.
     assert plan(1531, 1, 1531, -1) == _native.OK and kernels.CANDIDATES[out[0]].block_m == 64
+    # fp32: the 8-wave 256x256 tile takes no element loads of both operands
+    # (4-byte rows of an odd K above 128x128); AUTO plans another tile.
+    f32 = _native.DTYPE_F32
+    cid = kernels.config_id(next(c for c in kernels.candidates(torch.float32) if c.num_waves == 8), torch.float32)
+    big = lambda k, c: lib.forgeml_hip_gemm_plan(dummy, k, 1, dummy, 1, k, 4096, 4096, k, f32, c, out)  # noqa: E731
+    assert big(4095, cid) == _native.ECONFIG and "not built for this operand layout" in _native.last_error()
+    assert big(4096, cid) == _native.OK
+    assert big(4095, -1) == _native.OK and out[0] != cid
 
 
 def _gfx950_kernel_metadata(path):
