@@ -422,6 +422,10 @@ def test_residual_add_every_kernel(gpu, dtype):
             expected = _with_residual(reference_cpu(a, b, bias, activation), r)
             got = kernels.matmul(a_d, b_d, bias_d, activation=activation, residual=r.to(gpu))
             _gate(got, expected, k, what)
+            # The fused add is the GEMM's own output followed by torch's add:
+            # the same bits.
+            unfused = kernels.matmul(a_d, b_d, bias_d, activation=activation) + r.to(gpu)
+            assert torch.equal(got, unfused), f"{what}: fused residual differs from GEMM + add"
             # In place: the residual is the output buffer itself.
             out = r.to(gpu)
             kernels.matmul(a_d, b_d, bias_d, activation=activation, residual=out, out=out)
@@ -555,6 +559,7 @@ def test_eight_wave_tile(gpu, dtype, m, n, k):
     expected = reference_cpu(a, b, bias, "gelu") + r
     got = kernels.matmul(a_d, b_d, bias_d, activation="gelu", residual=r.to(gpu), config=cfg)
     _gate(got, expected, k, f"8-wave residual {m}x{n}x{k}")
+    assert torch.equal(got, kernels.matmul(a_d, b_d, bias_d, activation="gelu", config=cfg) + r.to(gpu))
     out = r.to(gpu)
     kernels.matmul(a_d, b_d, bias_d, activation="gelu", residual=out, out=out, config=cfg)
     _gate(out, expected, k, f"8-wave residual in place {m}x{n}x{k}")
